@@ -1,0 +1,242 @@
+"""Benchmark of the MI355X einsum path (one JSON line on stdout).
+
+Headline workload: BASELINE config 2, the transposing batched contraction
+``bji,bjk->bik`` in float32 with b=16, i=1000, j=777, k=1536 (standard-normal
+inputs from a seed).  A step is one ``run_einsum_exec`` over that batch with
+operands and output resident in HBM.  ``value`` is TFLOP/s over the timed
+steps (2*b*i*j*k flops per step).  ``roofline`` relates the GEMM kernel's
+average launch time (HIP events recorded around each launch on the launch
+stream) to the float32 MFMA peak.  ``cpu_baseline`` times the reference CPU
+route (cpu_einsum.h compiled by oracle/ref_build.py; the C restatement in
+oracle/ when that build is absent) on one of the 16 batches.
+
+``per_config`` adds every other BASELINE equation at full size with its own
+binding roof (HBM bytes or MFMA flops), measured the same way.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-configs]
+"""
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "pto-einsum_amd"))
+
+PEAK_HBM_GBS = 8000.0
+PEAK_TFLOPS = {"f32": 157.3, "f16": 2516.6}
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-configs", action="store_true", help="headline workload only")
+    ap.add_argument("--cpu-sample-batches", type=int, default=1)
+    return ap.parse_args()
+
+
+def time_runner(run, a, b, steps, warmup):
+    """Per-launch HIP-event times (ms) and wall time of the timed region."""
+    import torch
+
+    for _ in range(warmup):
+        run(a, b)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record(stream)
+    for s, e in ev:
+        s.record(stream)
+        run(a, b)
+        e.record(stream)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    per = [s.elapsed_time(e) for s, e in ev]
+    return per, t0.elapsed_time(t1)
+
+
+def config_list():
+    import torch
+
+    def randn(shape, g, scale=1.0, dtype=torch.float32):
+        return (torch.randn(shape, generator=g) * scale).to(dtype)
+
+    def decay(t, gamma):
+        i = torch.arange(t, dtype=torch.float64)
+        d = (i[:, None] - i[None, :])
+        return torch.where(d >= 0, gamma ** d.clamp(min=0), torch.zeros(())).float()
+
+    f16 = torch.float16
+    return [
+        ("1", "ij,jk->ik", lambda g: (torch.rand(256, 256, generator=g), torch.rand(256, 256, generator=g)), "f32"),
+        ("3", "bshd,bthd->bsht", lambda g: (randn((4, 2048, 32, 128), g, 128 ** -0.5, f16),
+                                            randn((4, 2048, 32, 128), g, 128 ** -0.5, f16)), "f16"),
+        ("4a", "ts,ts->ts", lambda g: (torch.rand(8192, 8192, generator=g), decay(8192, 0.99)), "f32"),
+        ("4b", "bsd,d->bsd", lambda g: (randn((8, 4096, 4096), g, 1.0, f16),
+                                        (torch.rand(4096, generator=g) + 0.5).to(f16)), "f16"),
+        ("5.1", "tn,sn->ts", lambda g: (randn((4096, 128), g, 128 ** -0.5, f16),
+                                        randn((4096, 128), g, 128 ** -0.5, f16)), "f16"),
+        ("5.2", "ts,ts->ts", lambda g: (torch.rand(4096, 4096, generator=g), decay(4096, 0.995)), "f32"),
+        ("5.3", "ts,sp->tp", lambda g: (torch.rand(4096, 4096, generator=g), randn((4096, 128), g)), "f32"),
+        ("5.R", "bshd,sd->bshd", lambda g: (randn((2, 4096, 32, 128), g, 1.0, f16), rope_table(4096, 128)), "f16"),
+    ]
+
+
+def rope_table(s, d):
+    import torch
+
+    pos = torch.arange(s, dtype=torch.float64)[:, None]
+    i = torch.arange(d, dtype=torch.float64)[None, :] % (d // 2)
+    theta = 10000.0 ** (-2.0 * i / d)
+    return torch.cos(pos * theta).to(torch.float16)
+
+
+def work(eq, a, b):
+    """(flops, compulsory bytes) of one einsum: 2*I*L0*L1*C (or N for a
+    product) and inputs read once plus the float32 output written once."""
+    from math import prod
+
+    t0, rest = eq.split(",")
+    t1, to = rest.split("->")
+    size = dict(zip(t0, a.shape))
+    size.update(zip(t1, b.shape))
+    out = prod(size[x] for x in to)
+    C = prod(size[x] for x in (set(t0) & set(t1)) - set(to))
+    flops = 2 * out * C if C > 1 else out
+    nbytes = a.numel() * a.element_size() + b.numel() * b.element_size() + out * 4
+    return flops, nbytes
+
+
+def roofline(flops, nbytes, t_ms, dtype):
+    tflops = flops / (t_ms * 1e-3) / 1e12
+    gbs = nbytes / (t_ms * 1e-3) / 1e9
+    t_mfma = flops / (PEAK_TFLOPS[dtype] * 1e12)
+    t_hbm = nbytes / (PEAK_HBM_GBS * 1e9)
+    if t_mfma >= t_hbm:
+        return dict(bound="mfma", achieved=round(tflops, 3), peak=PEAK_TFLOPS[dtype], unit="TFLOP/s",
+                    frac=round(tflops / PEAK_TFLOPS[dtype], 4)), tflops, gbs
+    return dict(bound="hbm", achieved=round(gbs, 1), peak=PEAK_HBM_GBS, unit="GB/s",
+                frac=round(gbs / PEAK_HBM_GBS, 4)), tflops, gbs
+
+
+def cpu_baseline(nbatch):
+    """Reference CPU route on `nbatch` of config 2's 16 batches, 1 thread."""
+    import numpy as np
+    import torch
+
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+    import ref_build
+
+    eq, s0, s1 = "bji,bjk->bik", (nbatch, 777, 1000), (nbatch, 777, 1536)
+    g = torch.Generator().manual_seed(1)
+    a = torch.randn(s0, generator=g).numpy()
+    b = torch.randn(s1, generator=g).numpy()
+    if os.path.exists(ref_build.so_path(eq, s0, s1)):
+        kind = "reference"
+        fn = lambda: ref_build.run(eq, a, b)  # noqa: E731
+    else:
+        kind = "port"
+        fn = lambda: oracle.einsum(eq, a, b)  # noqa: E731
+    t = time.perf_counter()
+    fn()
+    dt = time.perf_counter() - t
+    flops = 2.0 * nbatch * 1000 * 1536 * 777
+    return dict(value=round(flops / dt / 1e12, 6), unit="TFLOP/s", cores=1, kind=kind,
+                sample=(f"{nbatch} of 16 batches of config 2 (bji,bjk->bik float32, j=777, i=1000, "
+                        f"k=1536): {flops / 1e9:.2f} GFLOP in {dt:.2f} s on 1 thread of {os.cpu_count()}"),
+                seconds=round(dt, 3))
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(the contraction would shard on its batch axes with no exchange; see DESIGN.md).",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from pto_einsum import EinsumBuilder
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    # ---- headline: config 2 ----
+    eq, s0, s1 = "bji,bjk->bik", (16, 777, 1000), (16, 777, 1536)
+    g = torch.Generator().manual_seed(2)
+    a = torch.randn(s0, generator=g).to(dev)
+    b = torch.randn(s1, generator=g).to(dev)
+    log(f"bench: building {eq} {s0} x {s1} float32")
+    builder = EinsumBuilder(eq, [s0, s1], torch.float32)
+    run = builder.build()
+    log(f"bench: plan {builder.launch_plan.gemm} staged={builder.launch_plan.gather0 or builder.launch_plan.gather1 or builder.launch_plan.scatter_out}")
+    per, total_ms = time_runner(run, a, b, args.steps, args.warmup)
+    flops, nbytes = work(eq, a, b)
+    ms_per_step = total_ms / args.steps
+    kernel_ms = statistics.mean(per)
+    roof, _, _ = roofline(flops, nbytes, kernel_ms, "f32")
+    roof["traffic"] = None
+    value = flops / (ms_per_step * 1e-3) / 1e12
+    log(f"bench: config 2 {ms_per_step * 1e3:.1f} us/step, kernel {kernel_ms * 1e3:.1f} us, {value:.2f} TFLOP/s")
+
+    per_config = []
+    if not args.no_configs:
+        for name, ceq, gen, dt in config_list():
+            gg = torch.Generator().manual_seed(100 + len(per_config))
+            x, y = gen(gg)
+            x, y = x.to(dev), y.to(dev)
+            r = EinsumBuilder(ceq, [tuple(x.shape), tuple(y.shape)], x.dtype).build()
+            steps = max(5, args.steps // 2)
+            p, _ = time_runner(r, x, y, steps, max(3, args.warmup // 2))
+            f, nb = work(ceq, x, y)
+            km = statistics.median(p)
+            rf, tf, gb = roofline(f, nb, km, dt)
+            per_config.append(dict(config=name, equation=ceq, dtype=dt, us=round(km * 1e3, 2),
+                                   tflops=round(tf, 3), gbs=round(gb, 1), roof=rf["bound"],
+                                   frac=rf["frac"]))
+            log(f"bench: config {name} {ceq} {km * 1e3:.1f} us  {tf:.2f} TFLOP/s  {gb:.0f} GB/s  "
+                f"{rf['bound']} {rf['frac'] * 100:.1f}%")
+            del x, y, r
+            torch.cuda.empty_cache()
+
+    log("bench: timing the CPU baseline")
+    cpu = cpu_baseline(args.cpu_sample_batches)
+    log(f"bench: cpu baseline {cpu}")
+
+    line = {
+        "metric": "einsum TFLOP/s & HBM GB/s as % of MI355X roofline, per equation",
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded standard-normal operands, resident in HBM)",
+        "config": {"workload": "config 2: bji,bjk->bik float32 b=16 i=1000 j=777 k=1536",
+                   "equation": eq, "shapes": [list(s0), list(s1)], "parallelism": "single GPU"},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "per_config": per_config,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,156 @@
+/*
+ * pto_einsum_hip.h -- C ABI of the MI355X (gfx950) einsum backend.
+ *
+ * Two layers, both plain C (pointers, sizes, a void* hipStream_t):
+ *
+ *  1. Per-shape entry points.  Every JIT library the Python builder generates
+ *     for one (equation, shapes, dtype) exports exactly the symbol set the
+ *     reference binds through ctypes (reference builder.py:761-815; wrappers
+ *     in templates.py:74-92, 111-129, 158-191).  T is `float` or `uint16_t`
+ *     (IEEE half bits, the reference's ctypes c_uint16); outputs are float.
+ *     Where the reference returns void, these return 0 or a pe_status code.
+ *
+ *  2. The core library (libpto_einsum_hip.so) the per-shape wrappers call:
+ *     descriptor-driven launchers for the three kernel families (strided
+ *     product, permutation copy, batched MFMA GEMM) and the plan executor.
+ *
+ * Streams: `stream` is a hipStream_t (torch.cuda.current_stream().cuda_stream);
+ * NULL means the default stream.  All launches are asynchronous; nothing in
+ * an exec path allocates, frees or synchronizes.
+ */
+#ifndef PTO_EINSUM_HIP_H
+#define PTO_EINSUM_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PE_MAX_DIMS 8
+
+/* Status codes.  Positive values are hipError_t codes from the runtime. */
+enum pe_status {
+    PE_OK = 0,
+    PE_ERR_INVALID = -1,     /* descriptor inconsistent (message: pe_last_error) */
+    PE_ERR_BOUNDS = -2,      /* descriptor would address outside an operand */
+    PE_ERR_UNSUPPORTED = -3, /* dtype / rank / layout the kernels do not cover */
+    PE_ERR_WORKSPACE = -4    /* workspace missing or too small */
+};
+
+enum pe_dtype { PE_F32 = 0, PE_F16 = 1 };
+
+/* Contraction-free product over a row-major float32 output:
+ *   out[o] = (add_zero ? 0.0f + a*b : a*b),  a = (float)in0[sum_d o_d*a_stride[d]],
+ *                                           b = (float)in1[sum_d o_d*b_stride[d]].
+ * add_zero = 1 reproduces the reference CPU route's C=1 matmul accumulation
+ * (cpu_einsum.h:71-76: accum = 0; accum += a*b), 0 its Hadamard multiply
+ * (cpu_einsum.h:87-92).  Covers Hadamard, broadcast, outer and transposed
+ * elementwise products. */
+typedef struct pe_product_desc {
+    int32_t dtype;
+    int32_t add_zero;
+    int32_t ndims;                      /* 0..PE_MAX_DIMS */
+    int32_t _pad;
+    int64_t shape[PE_MAX_DIMS];         /* output extents, outermost first */
+    int64_t a_stride[PE_MAX_DIMS];      /* in0 element stride per output axis */
+    int64_t b_stride[PE_MAX_DIMS];      /* in1 element stride per output axis */
+    int64_t a_numel, b_numel;           /* operand extents, for bounds checks */
+} pe_product_desc;
+
+/* Permutation copy (bit-exact): dst is row-major over `shape`;
+ *   dst[o] = src[sum_d o_d * src_stride[d]]
+ * i.e. the reference's transfer_idx map with to_shape = shape and
+ * perm_strides = src_stride (cpu_einsum.h:35-51). */
+typedef struct pe_permute_desc {
+    int32_t elem_bytes;                 /* 2 or 4 */
+    int32_t ndims;
+    int64_t shape[PE_MAX_DIMS];
+    int64_t src_stride[PE_MAX_DIMS];
+    int64_t src_numel;
+} pe_permute_desc;
+
+/* Batched strided GEMM with float32 accumulation:
+ *   C[b,m,n] = sum_k (float)A[b,m,k] * (float)B[b,k,n]
+ * with A at a_off(b) + m*a_ms + k*a_ks, B at b_off(b) + k*b_ks + n*b_ns and
+ * C at c_off(b) + m*c_ms + n*c_ns, where x_off(b) decodes the flat batch
+ * index over batch_shape (row-major) with the per-axis x_bstride. */
+typedef struct pe_gemm_desc {
+    int32_t dtype;
+    int32_t nbatch;                     /* 0..PE_MAX_DIMS batch axes */
+    int32_t split_k;                    /* 0 = choose; else number of K splits */
+    int32_t tile;                       /* 0 = choose; else 64 or 128 (square) */
+    int64_t batch_shape[PE_MAX_DIMS];
+    int64_t a_bstride[PE_MAX_DIMS], b_bstride[PE_MAX_DIMS], c_bstride[PE_MAX_DIMS];
+    int64_t M, N, K;
+    int64_t a_ms, a_ks, b_ks, b_ns, c_ms, c_ns;
+    int64_t a_numel, b_numel, c_numel;
+} pe_gemm_desc;
+
+enum pe_route { PE_ROUTE_PRODUCT = 0, PE_ROUTE_GEMM = 1 };
+
+/* A whole einsum: either one product launch, or
+ *   [gather in0 -> ws] [gather in1 -> ws] GEMM [ws -> permute into out].
+ * Workspace regions are byte offsets into the buffer run_einsum_setup returns. */
+typedef struct pe_einsum_plan {
+    int32_t route;
+    int32_t gather0, gather1, scatter_out;  /* 1 = stage through workspace */
+    pe_product_desc product;
+    pe_permute_desc perm0, perm1, perm_out;
+    pe_gemm_desc gemm;
+    int64_t ws0_off, ws1_off, wsout_off, wsgemm_off;
+    int64_t ws_bytes;                     /* total workspace bytes */
+} pe_einsum_plan;
+
+/* ---- core library (libpto_einsum_hip.so) ---- */
+
+/* Launchers: validate the descriptor on the host, then enqueue on `stream`. */
+int pe_product(const pe_product_desc* d, const void* in0, const void* in1, float* out,
+               void* stream);
+int pe_permute(const pe_permute_desc* d, const void* src, void* dst, void* stream);
+int64_t pe_gemm_workspace_bytes(const pe_gemm_desc* d);
+int pe_gemm(const pe_gemm_desc* d, const void* a, const void* b, float* c, void* ws,
+            int64_t ws_bytes, void* stream);
+
+/* Plan executor: the body of every per-shape run_einsum_exec. */
+int pe_einsum_exec(const pe_einsum_plan* p, const void* in0, const void* in1, float* out,
+                   void* ws, void* stream);
+/* Allocates the plan's workspace (>= 256 bytes, never NULL on success). */
+void* pe_einsum_setup(const pe_einsum_plan* p, void* stream);
+/* Waits for the device, then frees a workspace from pe_einsum_setup. */
+int pe_einsum_teardown(void* ws);
+/* Synchronous one-shot: setup, exec, stream sync, teardown. */
+int pe_einsum_run(const pe_einsum_plan* p, const void* in0, const void* in1, float* out,
+                  void* stream);
+
+const char* pe_last_error(void);        /* message for the calling thread's last failure */
+int pe_device_cu_count(void);           /* compute units of the current device */
+const char* pe_version(void);
+
+/* ---- per-shape entry points (one JIT library per equation/shapes/dtype) ----
+ * Declared here with T = void; the generated source defines them with the
+ * element type of its dtype. */
+#ifndef PE_NO_PER_SHAPE_DECLS
+/* reference: templates.py:178-180 -> pto_einsum.h:283-290 (one-shot) */
+int run_einsum(const void* input0, const void* input1, float* output, void* stream);
+/* reference: templates.py:181-183 -> pto_einsum.h:207-248 */
+void* run_einsum_setup(void* stream);
+/* reference: templates.py:184-186 -> pto_einsum.h:253-275 */
+int run_einsum_exec(const void* input0, const void* input1, float* output, void* workspace,
+                    void* stream);
+/* reference: templates.py:187-189 -> pto_einsum.h:277-279 */
+void run_einsum_teardown(void* workspace);
+/* reference: templates.py:166-171 -> pto_einsum_transpose.h:662-678 */
+int run_transpose_inp0(const void* input, void* output, void* stream);
+int run_transpose_inp1(const void* input, void* output, void* stream);
+/* reference: templates.py:172-174 */
+int run_transpose_out(const float* input, float* output, void* stream);
+/* reference: templates.py:175-177 -> pto_einsum_matmul.h:973-1027 */
+int run_batched_matmul(const void* ws0, const void* ws1, float* ws_res, void* stream);
+#endif
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PTO_EINSUM_HIP_H */

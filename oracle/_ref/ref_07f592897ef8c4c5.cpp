@@ -1,0 +1,42 @@
+#include "cpu_einsum.h"
+
+struct config_tpose_inp0 {
+    static constexpr unsigned dims = 2;
+    static constexpr unsigned N = 2048;
+    static constexpr unsigned from_shape[2] = {32, 64};
+    static constexpr unsigned to_shape[2] = {32, 64};
+    static constexpr unsigned perm[2] = {0, 1};
+    static constexpr unsigned perm_strides[2] = {64, 1};
+};
+
+struct config_tpose_inp1 {
+    static constexpr unsigned dims = 1;
+    static constexpr unsigned N = 64;
+    static constexpr unsigned from_shape[1] = {64};
+    static constexpr unsigned to_shape[1] = {64};
+    static constexpr unsigned perm[1] = {0};
+    static constexpr unsigned perm_strides[1] = {1};
+};
+
+struct config_tpose_out {
+    static constexpr unsigned dims = 1;
+    static constexpr unsigned N = 32;
+    static constexpr unsigned from_shape[1] = {32};
+    static constexpr unsigned to_shape[1] = {32};
+    static constexpr unsigned perm[1] = {0};
+    static constexpr unsigned perm_strides[1] = {1};
+};
+
+struct config_einsum {
+    typedef config_tpose_inp0 tpose_inp0_config;
+    typedef config_tpose_inp1 tpose_inp1_config;
+    typedef config_tpose_out tpose_out_conf;
+    static const unsigned n_free0 = 32;
+    static const unsigned n_free1 = 1;
+    static const unsigned n_contract = 64;
+    static const unsigned n_inplace = 1;
+};
+
+extern "C" void run_einsum(const float* input0, const float* input1, float* output, void* stream) {
+    cpu::einsum<float, config_einsum>(input0, input1, output);
+}

@@ -1,0 +1,42 @@
+#include "cpu_einsum.h"
+
+struct config_tpose_inp0 {
+    static constexpr unsigned dims = 2;
+    static constexpr unsigned N = 5120;
+    static constexpr unsigned from_shape[2] = {160, 32};
+    static constexpr unsigned to_shape[2] = {160, 32};
+    static constexpr unsigned perm[2] = {0, 1};
+    static constexpr unsigned perm_strides[2] = {32, 1};
+};
+
+struct config_tpose_inp1 {
+    static constexpr unsigned dims = 2;
+    static constexpr unsigned N = 4608;
+    static constexpr unsigned from_shape[2] = {144, 32};
+    static constexpr unsigned to_shape[2] = {32, 144};
+    static constexpr unsigned perm[2] = {1, 0};
+    static constexpr unsigned perm_strides[2] = {1, 32};
+};
+
+struct config_tpose_out {
+    static constexpr unsigned dims = 2;
+    static constexpr unsigned N = 23040;
+    static constexpr unsigned from_shape[2] = {160, 144};
+    static constexpr unsigned to_shape[2] = {160, 144};
+    static constexpr unsigned perm[2] = {0, 1};
+    static constexpr unsigned perm_strides[2] = {144, 1};
+};
+
+struct config_einsum {
+    typedef config_tpose_inp0 tpose_inp0_config;
+    typedef config_tpose_inp1 tpose_inp1_config;
+    typedef config_tpose_out tpose_out_conf;
+    static const unsigned n_free0 = 160;
+    static const unsigned n_free1 = 144;
+    static const unsigned n_contract = 32;
+    static const unsigned n_inplace = 1;
+};
+
+extern "C" void run_einsum(const float* input0, const float* input1, float* output, void* stream) {
+    cpu::einsum<float, config_einsum>(input0, input1, output);
+}

@@ -1,0 +1,101 @@
+// Shared helpers for the gfx950 einsum kernels: error reporting, integer
+// division by run-time constants, vector types and launch utilities.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "pto_einsum_hip.h"
+
+namespace pe {
+
+// ---------------------------------------------------------------- errors --
+
+// Records a message for pe_last_error() and returns `code`.
+int fail(int code, const std::string& msg);
+int hip_status(hipError_t e, const char* what);
+
+#define PE_CHECK_HIP(expr)                                       \
+    do {                                                         \
+        hipError_t _e = (expr);                                  \
+        if (_e != hipSuccess) return ::pe::hip_status(_e, #expr); \
+    } while (0)
+
+// ------------------------------------------------- division by constants --
+
+// Unsigned 32-bit division by a run-time constant d >= 1 via one multiply-high
+// (Granlund & Montgomery, "Division by invariant integers using
+// multiplication", PLDI 1994, round-up variant): with l = ceil(log2 d) and
+// m = floor(2^32 * (2^l - d) / d) + 1, q = (mulhi(n, m) + n) >> l for all
+// n < 2^32.  The 33-bit sum is formed as t + ((n - t) >> 1) to stay in 32 bits.
+struct FastDiv {
+    uint32_t d;
+    uint32_t m;
+    uint32_t s;  // l
+    FastDiv() : d(1), m(0), s(0) {}
+    explicit FastDiv(uint32_t div) { init(div); }
+    void init(uint32_t div) {
+        d = div ? div : 1;
+        uint32_t l = 0;
+        while (l < 32 && (uint64_t(1) << l) < d) ++l;
+        s = l;
+        m = uint32_t(((uint64_t(1) << 32) * ((uint64_t(1) << l) - d)) / d + 1);
+    }
+    __host__ __device__ __forceinline__ uint32_t div(uint32_t n) const {
+#if defined(__HIP_DEVICE_COMPILE__)
+        uint32_t t = __umulhi(n, m);
+#else
+        uint32_t t = uint32_t((uint64_t(n) * m) >> 32);
+#endif
+        if (s == 0) return n;  // d == 1
+        return (t + ((n - t) >> 1)) >> (s - 1);
+    }
+    __host__ __device__ __forceinline__ void divmod(uint32_t n, uint32_t& q, uint32_t& r) const {
+        q = div(n);
+        r = n - q * d;
+    }
+};
+
+// ------------------------------------------------------------ vectors --
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Element type tags: storage type and exact conversion to float.
+struct F32 {
+    using T = float;
+    static constexpr int kBytes = 4;
+    __device__ __forceinline__ static float to_f32(float x) { return x; }
+};
+struct F16 {
+    using T = _Float16;
+    static constexpr int kBytes = 2;
+    __device__ __forceinline__ static float to_f32(_Float16 x) { return (float)x; }
+};
+
+__device__ __forceinline__ void store_nt(float* p, float v) {
+    __builtin_nontemporal_store(v, p);
+}
+__device__ __forceinline__ void store_nt(f32x4* p, f32x4 v) {
+    __builtin_nontemporal_store(v, p);
+}
+
+// --------------------------------------------------------------- device --
+
+// Number of compute units of the current device (memoised per device).
+int cu_count();
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+inline bool aligned(const void* p, size_t bytes) {
+    return (reinterpret_cast<uintptr_t>(p) % bytes) == 0;
+}
+
+}  // namespace pe

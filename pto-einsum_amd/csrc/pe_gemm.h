@@ -1,0 +1,79 @@
+// Batched strided GEMM on CDNA4 matrix cores (gfx950).
+//
+// Reference counterparts: batched_matmul_inline and its tile schedules
+// (pto_einsum_matmul.h:115-970) plus the operand transposes of Phase A
+// (pto_einsum_transpose.h) and the fused permuted store
+// (pto_einsum_matmul.h:614-639).  Here one kernel reads both operands at
+// their own strides (any of the reference's NT / NN-strided / TN direct-read
+// modes and the identity case, plus the transposed reads the reference
+// gathers first) and stores each tile straight into the permuted output.
+//
+//   C[b, m, n] = sum_k A[b, m, k] * B[b, k, n]      (float32 accumulation)
+//
+// Tiling: a 256-thread block (four 64-wide waves, 2x2) owns a BM x BN output
+// tile and walks K in BK slabs through double-buffered LDS.  Each wave owns
+// (BM/2) x (BN/2) as 32x32 MFMA blocks:
+//   float32: v_mfma_f32_32x32x2_f32  (2 k per instruction)
+//   float16: v_mfma_f32_32x32x16_f16 (16 k per instruction, gfx950)
+// Operand layouts in LDS are chosen so each lane's MFMA fragment is one LDS
+// read: float32 keeps [BK][BM] (lanes read 32 consecutive m), float16 keeps
+// [BM][BK] (each lane reads 8 consecutive k as one 16-byte read).
+//
+// Boundaries: rows m >= M and columns n >= N of a partial tile load clamped
+// (in-bounds, arbitrary) data -- they only feed outputs that are never
+// stored.  The K tail is zero-filled in both operands, so no garbage value
+// (not even inf/NaN) reaches a stored sum.  Every batch count and every
+// M/N/K works, including the batched partial tiles the reference rejects
+// (builder.py:593-604).
+//
+// Thin grids use a deterministic split-K: each split writes its partial tile
+// to a workspace slab and a second kernel sums the slabs in split order.
+#pragma once
+
+#include "pe_common.h"
+
+namespace pe {
+
+// Operand layout classes (chosen on the host from the strides).
+enum Layout : int {
+    L_GENERIC = 0,  // element-wise loads at arbitrary strides
+    L_MN = 1,       // m (A) / n (B) contiguous, 16-byte vectors along it
+    L_K = 2         // k contiguous, 16-byte vectors along k
+};
+
+struct GemmArgs {
+    const void* a;
+    const void* b;
+    float* c;
+    float* partial;           // split-K workspace, [split][batch][M][N]
+    int32_t M, N, K;
+    int32_t nsplit;
+    int32_t k_per_split;      // multiple of BK
+    int32_t tiles_m, tiles_n;
+    uint32_t tiles_per_batch; // tiles_m * tiles_n
+    uint32_t nbatch_total;
+    uint32_t total_blocks;    // tiles_per_batch * nbatch_total * nsplit
+    int64_t a_ms, a_ks, b_ks, b_ns, c_ms, c_ns;
+    int32_t nbatch;
+    FastDiv batch_div[PE_MAX_DIMS];
+    int64_t a_bs[PE_MAX_DIMS], b_bs[PE_MAX_DIMS], c_bs[PE_MAX_DIMS];
+};
+
+struct ReduceArgs {
+    const float* partial;
+    float* c;
+    int32_t nsplit;
+    uint32_t per_split;       // nbatch_total * M * N
+    FastDiv n_div, m_div;     // flat -> (batch, m, n)
+    int64_t c_ms, c_ns;
+    int32_t nbatch;
+    FastDiv batch_div[PE_MAX_DIMS];
+    int64_t c_bs[PE_MAX_DIMS];
+};
+
+// Host-side launch entry for one (dtype, tile) family; defined per family
+// in pe_gemm_f32.hip / pe_gemm_f16.hip.
+hipError_t launch_gemm_f32(int bm, int alayout, int blayout, const GemmArgs& g, hipStream_t s);
+hipError_t launch_gemm_f16(int bm, int alayout, int blayout, const GemmArgs& g, hipStream_t s);
+
+}  // namespace pe

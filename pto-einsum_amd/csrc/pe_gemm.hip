@@ -1,0 +1,205 @@
+// Host side of the batched MFMA GEMM: descriptor validation, operand layout
+// classification, tile / split-K choice and the deterministic split-K
+// reduction kernel.
+#include "pe_gemm.h"
+
+#include <algorithm>
+
+namespace pe {
+
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(ReduceArgs r) {
+    const uint32_t stride = gridDim.x * 256;
+    for (uint32_t idx = blockIdx.x * 256 + threadIdx.x; idx < r.per_split; idx += stride) {
+        float acc = 0.0f;
+        for (int s = 0; s < r.nsplit; ++s) acc = acc + r.partial[int64_t(s) * r.per_split + idx];
+        uint32_t rest, n, batch, m;
+        r.n_div.divmod(idx, rest, n);
+        r.m_div.divmod(rest, batch, m);
+        int64_t off = int64_t(m) * r.c_ms + int64_t(n) * r.c_ns;
+        for (int d = r.nbatch - 1; d >= 0; --d) {
+            uint32_t q, rr;
+            r.batch_div[d].divmod(batch, q, rr);
+            off += int64_t(rr) * r.c_bs[d];
+            batch = q;
+        }
+        store_nt(r.c + off, acc);
+    }
+}
+
+namespace {
+
+struct GemmChoice {
+    int bm;        // square tile edge, 64 or 128
+    int nsplit;    // K splits (1 = direct store)
+    int k_per_split;
+    int64_t nbatch_total;
+    int64_t ws_bytes;
+};
+
+int64_t batch_total(const pe_gemm_desc& d) {
+    int64_t n = 1;
+    for (int k = 0; k < d.nbatch; ++k) n *= d.batch_shape[k];
+    return n;
+}
+
+GemmChoice choose(const pe_gemm_desc& d) {
+    GemmChoice c{};
+    c.nbatch_total = batch_total(d);
+    const int bk = d.dtype == PE_F32 ? 16 : 32;
+    const int64_t cus = cu_count();
+    if (d.tile == 64 || d.tile == 128) {
+        c.bm = d.tile;
+    } else {
+        c.bm = (d.M > 64 && d.N > 64) ? 128 : 64;
+        if (c.bm == 128 && c.nbatch_total * ceil_div(d.M, 128) * ceil_div(d.N, 128) < cus) c.bm = 64;
+    }
+    const int64_t tiles = c.nbatch_total * ceil_div(d.M, c.bm) * ceil_div(d.N, c.bm);
+    int64_t split = 1;
+    if (d.split_k > 0) {
+        split = d.split_k;
+    } else if (tiles < cus && c.nbatch_total * d.M * d.N < (int64_t(1) << 32)) {
+        // Fill about two blocks per CU, keeping at least four K slabs per split.
+        split = std::min<int64_t>(ceil_div(2 * cus, tiles), std::max<int64_t>(1, d.K / (4 * bk)));
+        split = std::max<int64_t>(1, std::min<int64_t>(split, 32));
+    }
+    int64_t kps = ceil_div(ceil_div(d.K, split), bk) * bk;
+    split = std::max<int64_t>(1, ceil_div(d.K, kps));
+    c.nsplit = int(split);
+    c.k_per_split = int(kps);
+    c.ws_bytes = split > 1 ? split * c.nbatch_total * d.M * d.N * int64_t(sizeof(float)) : 0;
+    return c;
+}
+
+int classify(int64_t rows, int64_t k, int64_t rs, int64_t ks, const int64_t* bs, int nb,
+             const void* p, int vec) {
+    // Extent-1 axes carry no stride; treat them as absent.
+    if (rows == 1) rs = 0;
+    if (k == 1) ks = 0;
+    bool batch_ok = true;
+    for (int i = 0; i < nb; ++i) batch_ok = batch_ok && (bs[i] % vec == 0);
+    const bool al = aligned(p, 16) && batch_ok;
+    if (rs == 1 && ks % vec == 0 && al) return L_MN;
+    if (ks == 1 && rs % vec == 0 && al) return L_K;
+    return L_GENERIC;
+}
+
+}  // namespace
+
+int validate_gemm(const pe_gemm_desc& d) {
+    if (d.dtype != PE_F32 && d.dtype != PE_F16)
+        return fail(PE_ERR_UNSUPPORTED, "gemm: dtype must be PE_F32 or PE_F16");
+    if (d.nbatch < 0 || d.nbatch > PE_MAX_DIMS) return fail(PE_ERR_INVALID, "gemm: nbatch out of range");
+    if (d.M < 0 || d.N < 0 || d.K < 0) return fail(PE_ERR_INVALID, "gemm: negative extent");
+    if (d.M >= (int64_t(1) << 31) || d.N >= (int64_t(1) << 31) || d.K >= (int64_t(1) << 31))
+        return fail(PE_ERR_UNSUPPORTED, "gemm: M, N and K must each be below 2^31");
+    int64_t amax = 0, bmax = 0, cmax = 0, nb = 1;
+    for (int i = 0; i < d.nbatch; ++i) {
+        if (d.batch_shape[i] < 0 || d.a_bstride[i] < 0 || d.b_bstride[i] < 0 || d.c_bstride[i] < 0)
+            return fail(PE_ERR_INVALID, "gemm: negative batch extent or stride");
+        nb *= d.batch_shape[i];
+        if (d.batch_shape[i] > 0) {
+            amax += (d.batch_shape[i] - 1) * d.a_bstride[i];
+            bmax += (d.batch_shape[i] - 1) * d.b_bstride[i];
+            cmax += (d.batch_shape[i] - 1) * d.c_bstride[i];
+        }
+    }
+    if (nb >= (int64_t(1) << 31)) return fail(PE_ERR_UNSUPPORTED, "gemm: batch count must be below 2^31");
+    if (d.a_ms < 0 || d.a_ks < 0 || d.b_ks < 0 || d.b_ns < 0 || d.c_ms < 0 || d.c_ns < 0)
+        return fail(PE_ERR_INVALID, "gemm: negative stride");
+    if (nb == 0 || d.M == 0 || d.N == 0) return PE_OK;
+    cmax += (d.M - 1) * d.c_ms + (d.N - 1) * d.c_ns;
+    if (cmax >= d.c_numel) return fail(PE_ERR_BOUNDS, "gemm: C strides address past the output");
+    if (d.K > 0) {
+        amax += (d.M - 1) * d.a_ms + (d.K - 1) * d.a_ks;
+        bmax += (d.N - 1) * d.b_ns + (d.K - 1) * d.b_ks;
+        if (amax >= d.a_numel) return fail(PE_ERR_BOUNDS, "gemm: A strides address past operand 0");
+        if (bmax >= d.b_numel) return fail(PE_ERR_BOUNDS, "gemm: B strides address past operand 1");
+    }
+    const int64_t tiles = nb * ceil_div(d.M, 64) * ceil_div(d.N, 64) * 32;
+    if (tiles >= (int64_t(1) << 32)) return fail(PE_ERR_UNSUPPORTED, "gemm: too many tiles");
+    return PE_OK;
+}
+
+}  // namespace pe
+
+extern "C" int64_t pe_gemm_workspace_bytes(const pe_gemm_desc* d) {
+    if (!d || pe::validate_gemm(*d) != PE_OK) return 0;
+    if (d->K == 0) return 0;
+    return pe::choose(*d).ws_bytes;
+}
+
+extern "C" int pe_gemm(const pe_gemm_desc* d, const void* a, const void* b, float* c, void* ws,
+                       int64_t ws_bytes, void* stream) {
+    using namespace pe;
+    if (!d) return fail(PE_ERR_INVALID, "gemm: null descriptor");
+    int st = validate_gemm(*d);
+    if (st != PE_OK) return st;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int64_t nb = batch_total(*d);
+    if (nb == 0 || d->M == 0 || d->N == 0) return PE_OK;
+
+    ReduceArgs r{};
+    r.c = c;
+    r.per_split = uint32_t(nb * d->M * d->N);
+    r.n_div.init(uint32_t(d->N));
+    r.m_div.init(uint32_t(d->M));
+    r.c_ms = d->c_ms;
+    r.c_ns = d->c_ns;
+    r.nbatch = d->nbatch;
+    for (int i = 0; i < d->nbatch; ++i) {
+        r.batch_div[i].init(uint32_t(d->batch_shape[i]));
+        r.c_bs[i] = d->c_bstride[i];
+    }
+    auto reduce_grid = [&]() {
+        return int(std::max<int64_t>(1, std::min<int64_t>(ceil_div(r.per_split, 256), cu_count() * 8)));
+    };
+    if (d->K == 0) {  // empty contraction: every output is the empty sum, +0
+        if (nb * d->M * d->N >= (int64_t(1) << 32)) return fail(PE_ERR_UNSUPPORTED, "gemm: output too large");
+        r.nsplit = 0;
+        r.partial = nullptr;
+        hipLaunchKernelGGL(splitk_reduce_kernel, dim3(reduce_grid()), dim3(256), 0, s, r);
+        PE_CHECK_HIP(hipGetLastError());
+        return PE_OK;
+    }
+
+    GemmChoice ch = choose(*d);
+    if (ch.nsplit > 1) {
+        if (!ws || ws_bytes < ch.ws_bytes) return fail(PE_ERR_WORKSPACE, "gemm: split-K workspace missing or too small");
+        if (nb * d->M * d->N >= (int64_t(1) << 32))
+            return fail(PE_ERR_UNSUPPORTED, "gemm: split-K output too large");
+    }
+    const int vec = d->dtype == PE_F32 ? 4 : 8;
+    const int al = classify(d->M, d->K, d->a_ms, d->a_ks, d->a_bstride, d->nbatch, a, vec);
+    const int bl = classify(d->N, d->K, d->b_ns, d->b_ks, d->b_bstride, d->nbatch, b, vec);
+
+    GemmArgs g{};
+    g.a = a; g.b = b; g.c = c;
+    g.partial = static_cast<float*>(ws);
+    g.M = int32_t(d->M); g.N = int32_t(d->N); g.K = int32_t(d->K);
+    g.nsplit = ch.nsplit;
+    g.k_per_split = ch.k_per_split;
+    g.tiles_m = int32_t(ceil_div(d->M, ch.bm));
+    g.tiles_n = int32_t(ceil_div(d->N, ch.bm));
+    g.tiles_per_batch = uint32_t(g.tiles_m) * uint32_t(g.tiles_n);
+    g.nbatch_total = uint32_t(nb);
+    g.total_blocks = g.tiles_per_batch * g.nbatch_total * uint32_t(ch.nsplit);
+    g.a_ms = d->a_ms; g.a_ks = d->a_ks; g.b_ks = d->b_ks; g.b_ns = d->b_ns;
+    g.c_ms = d->c_ms; g.c_ns = d->c_ns;
+    g.nbatch = d->nbatch;
+    for (int i = 0; i < d->nbatch; ++i) {
+        g.batch_div[i].init(uint32_t(d->batch_shape[i]));
+        g.a_bs[i] = d->a_bstride[i];
+        g.b_bs[i] = d->b_bstride[i];
+        g.c_bs[i] = d->c_bstride[i];
+    }
+    hipError_t e = d->dtype == PE_F32 ? launch_gemm_f32(ch.bm, al, bl, g, s)
+                                      : launch_gemm_f16(ch.bm, al, bl, g, s);
+    PE_CHECK_HIP(e);
+    if (ch.nsplit > 1) {
+        r.nsplit = ch.nsplit;
+        r.partial = static_cast<const float*>(ws);
+        hipLaunchKernelGGL(splitk_reduce_kernel, dim3(reduce_grid()), dim3(256), 0, s, r);
+        PE_CHECK_HIP(hipGetLastError());
+    }
+    return PE_OK;
+}

@@ -1,0 +1,277 @@
+// Permutation copies (bit-exact) of 2- and 4-byte elements.
+//
+// Reference counterpart: transpose_inline and its bodies
+// (pto_einsum_transpose.h:27-660): identity copy, N-D gather with the
+// innermost axis kept, and 2D / batched-2D TTRANS when the innermost axis
+// moves.  The destination is row-major over `shape`; destination axis d reads
+// the source with stride src_stride[d] -- the transfer_idx map of
+// cpu_einsum.h:35-43.
+//
+// After merging axes that stay adjacent (and dropping extent-1 axes) there
+// are two cases, both HBM-bound (one read and one write per element):
+//  * the innermost destination axis is also source-contiguous: a streamed
+//    gather of contiguous runs with 16-byte vectors where the run length and
+//    strides allow it;
+//  * otherwise a 64x64 LDS-tiled transpose between the destination's
+//    innermost axis and the axis that is contiguous in the source, with the
+//    remaining axes decoded from blockIdx.  Both global sides are coalesced;
+//    the LDS tile has one padding column so the transposed read is free of
+//    bank conflicts.
+#include "pe_common.h"
+
+#include <algorithm>
+#include <vector>
+
+namespace pe {
+namespace {
+
+constexpr int kThreads = 256;
+
+struct GatherArgs {
+    const void* src;
+    void* dst;
+    uint32_t nvec;           // destination vectors (32-bit path)
+    FastDiv inner_vecs;      // innermost extent / VEC
+    int32_t nouter;
+    FastDiv outer_div[PE_MAX_DIMS];
+    int64_t outer_stride[PE_MAX_DIMS];
+    int64_t inner_stride;    // source stride of the innermost destination axis
+};
+
+template <typename W, int VEC>
+struct Chunk {
+    W v[VEC];
+};
+
+// Streamed gather: VEC elements of type W per vector (16 bytes when VEC > 1).
+template <typename W, int VEC, bool HAS_OUTER>
+__global__ __launch_bounds__(kThreads) void gather_kernel(GatherArgs p) {
+    const W* __restrict__ src = static_cast<const W*>(p.src);
+    W* __restrict__ dst = static_cast<W*>(p.dst);
+    const uint32_t stride = gridDim.x * kThreads;
+    for (uint32_t v = blockIdx.x * kThreads + threadIdx.x; v < p.nvec; v += stride) {
+        int64_t off;
+        if constexpr (HAS_OUTER) {
+            uint32_t row, colv;
+            p.inner_vecs.divmod(v, row, colv);
+            off = int64_t(colv) * VEC * p.inner_stride;
+            for (int d = p.nouter - 1; d >= 0; --d) {
+                uint32_t q, r;
+                p.outer_div[d].divmod(row, q, r);
+                off += int64_t(r) * p.outer_stride[d];
+                row = q;
+            }
+        } else {
+            off = int64_t(v) * VEC * p.inner_stride;
+        }
+        if constexpr (VEC > 1) {
+            using V = Chunk<W, VEC>;
+            *reinterpret_cast<V*>(dst + int64_t(v) * VEC) = *reinterpret_cast<const V*>(src + off);
+        } else {
+            dst[v] = src[off];
+        }
+    }
+}
+
+struct TileArgs {
+    const void* src;
+    void* dst;
+    int64_t P, Q;            // extents of the source-contiguous axis p and the
+                             // destination-innermost axis q
+    int64_t src_q_stride;    // source stride of q (p has source stride 1)
+    int64_t dst_p_stride;    // destination stride of p (q has destination stride 1)
+    uint32_t tiles_p, tiles_q;
+    int32_t nbatch;          // remaining axes, decoded from the batch index
+    FastDiv batch_div[PE_MAX_DIMS];
+    int64_t batch_src[PE_MAX_DIMS];
+    int64_t batch_dst[PE_MAX_DIMS];
+    uint32_t nbatch_total;
+};
+
+constexpr int kTile = 64;
+
+// One 64x64 tile per block: 256 threads read 64 rows (q) of 64 source-
+// contiguous elements (p), then write 64 rows (p) of 64 destination-
+// contiguous elements (q).
+template <typename W>
+__global__ __launch_bounds__(kThreads) void tile_transpose_kernel(TileArgs p) {
+    __shared__ W tile[kTile][kTile + 1];
+    const W* __restrict__ src = static_cast<const W*>(p.src);
+    W* __restrict__ dst = static_cast<W*>(p.dst);
+    const uint32_t tiles_per_batch = p.tiles_p * p.tiles_q;
+    const uint32_t total = tiles_per_batch * p.nbatch_total;
+    const int tx = threadIdx.x % kTile;
+    const int ty = threadIdx.x / kTile;  // 0..3
+    for (uint32_t t = blockIdx.x; t < total; t += gridDim.x) {
+        uint32_t bidx = t / tiles_per_batch;
+        uint32_t rem = t - bidx * tiles_per_batch;
+        uint32_t tq = rem / p.tiles_p;
+        uint32_t tp = rem - tq * p.tiles_p;
+        int64_t sbase = 0, dbase = 0;
+        for (int d = p.nbatch - 1; d >= 0; --d) {
+            uint32_t q, r;
+            p.batch_div[d].divmod(bidx, q, r);
+            sbase += int64_t(r) * p.batch_src[d];
+            dbase += int64_t(r) * p.batch_dst[d];
+            bidx = q;
+        }
+        const int64_t p0 = int64_t(tp) * kTile, q0 = int64_t(tq) * kTile;
+        const int64_t pi = p0 + tx;
+#pragma unroll
+        for (int r = 0; r < kTile / 4; ++r) {
+            int64_t qi = q0 + ty + 4 * r;
+            if (pi < p.P && qi < p.Q) tile[ty + 4 * r][tx] = src[sbase + qi * p.src_q_stride + pi];
+        }
+        __syncthreads();
+        const int64_t qo = q0 + tx;
+#pragma unroll
+        for (int r = 0; r < kTile / 4; ++r) {
+            int64_t po = p0 + ty + 4 * r;
+            if (po < p.P && qo < p.Q) dst[dbase + po * p.dst_p_stride + qo] = tile[tx][ty + 4 * r];
+        }
+        __syncthreads();
+    }
+}
+
+// Wide fallback (2^31+ elements): one element per thread, 64-bit decode.
+template <typename W>
+__global__ __launch_bounds__(kThreads) void gather_wide_kernel(const W* __restrict__ src,
+                                                               W* __restrict__ dst, int64_t n,
+                                                               pe_permute_desc d) {
+    const int64_t stride = int64_t(gridDim.x) * kThreads;
+    for (int64_t o = int64_t(blockIdx.x) * kThreads + threadIdx.x; o < n; o += stride) {
+        int64_t rem = o, off = 0;
+        for (int k = d.ndims - 1; k >= 0; --k) {
+            off += (rem % d.shape[k]) * d.src_stride[k];
+            rem /= d.shape[k];
+        }
+        dst[o] = src[off];
+    }
+}
+
+int grid_cap(int64_t blocks) {
+    int64_t cap = int64_t(cu_count()) * 16;
+    return int(std::max<int64_t>(1, std::min(blocks, cap)));
+}
+
+template <typename W>
+int run(const pe_permute_desc& d, const void* src, void* dst, hipStream_t s) {
+    // Merge destination-adjacent axes that are also source-adjacent.
+    std::vector<int64_t> shape, sst;
+    for (int k = 0; k < d.ndims; ++k) {
+        if (d.shape[k] == 1) continue;
+        if (!shape.empty() && sst.back() == d.shape[k] * d.src_stride[k]) {
+            shape.back() *= d.shape[k];
+            sst.back() = d.src_stride[k];
+        } else {
+            shape.push_back(d.shape[k]);
+            sst.push_back(d.src_stride[k]);
+        }
+    }
+    int64_t n = 1;
+    for (int64_t x : shape) n *= x;
+    if (n == 0) return PE_OK;
+    const int nd = int(shape.size());
+    if (n >= (int64_t(1) << 31)) {
+        pe_permute_desc m = d;
+        m.ndims = nd;
+        for (int k = 0; k < nd; ++k) { m.shape[k] = shape[k]; m.src_stride[k] = sst[k]; }
+        hipLaunchKernelGGL((gather_wide_kernel<W>), dim3(grid_cap(ceil_div(n, kThreads))),
+                           dim3(kThreads), 0, s, (const W*)src, (W*)dst, n, m);
+        PE_CHECK_HIP(hipGetLastError());
+        return PE_OK;
+    }
+    // Destination row-major strides of the merged axes.
+    std::vector<int64_t> dst_stride(nd, 1);
+    for (int k = nd - 2; k >= 0; --k) dst_stride[k] = dst_stride[k + 1] * shape[k + 1];
+
+    int pax = -1;  // merged axis with source stride 1
+    for (int k = 0; k < nd; ++k)
+        if (sst[k] == 1) pax = k;
+    const bool inner_kept = nd == 0 || sst[nd - 1] == 1;
+
+    if (inner_kept || pax < 0) {
+        GatherArgs a{};
+        a.src = src; a.dst = dst;
+        const int64_t inner = nd ? shape[nd - 1] : 1;
+        a.inner_stride = nd ? sst[nd - 1] : 0;
+        a.nouter = std::max(0, nd - 1);
+        for (int k = 0; k < a.nouter; ++k) {
+            a.outer_div[k].init(uint32_t(shape[k]));
+            a.outer_stride[k] = sst[k];
+        }
+        constexpr int VEC = 16 / sizeof(W);
+        bool vec = inner_kept && nd > 0 && inner % VEC == 0 && aligned(src, 16) && aligned(dst, 16);
+        for (int k = 0; k < a.nouter && vec; ++k) vec = sst[k] % VEC == 0;
+        const bool outer = a.nouter > 0;
+        if (vec) {
+            a.nvec = uint32_t(n / VEC);
+            a.inner_vecs.init(uint32_t(inner / VEC));
+            int grid = grid_cap(ceil_div(a.nvec, kThreads));
+            if (outer) hipLaunchKernelGGL((gather_kernel<W, VEC, true>), dim3(grid), dim3(kThreads), 0, s, a);
+            else hipLaunchKernelGGL((gather_kernel<W, VEC, false>), dim3(grid), dim3(kThreads), 0, s, a);
+        } else {
+            a.nvec = uint32_t(n);
+            a.inner_vecs.init(uint32_t(inner));
+            int grid = grid_cap(ceil_div(a.nvec, kThreads));
+            if (outer) hipLaunchKernelGGL((gather_kernel<W, 1, true>), dim3(grid), dim3(kThreads), 0, s, a);
+            else hipLaunchKernelGGL((gather_kernel<W, 1, false>), dim3(grid), dim3(kThreads), 0, s, a);
+        }
+        PE_CHECK_HIP(hipGetLastError());
+        return PE_OK;
+    }
+
+    // Tiled transpose between axis q = nd-1 (destination-contiguous) and pax.
+    const int qax = nd - 1;
+    TileArgs t{};
+    t.src = src; t.dst = dst;
+    t.P = shape[pax]; t.Q = shape[qax];
+    t.src_q_stride = sst[qax];
+    t.dst_p_stride = dst_stride[pax];
+    t.tiles_p = uint32_t(ceil_div(t.P, kTile));
+    t.tiles_q = uint32_t(ceil_div(t.Q, kTile));
+    int nb = 0;
+    int64_t nbt = 1;
+    for (int k = 0; k < nd; ++k) {
+        if (k == pax || k == qax) continue;
+        t.batch_div[nb].init(uint32_t(shape[k]));
+        t.batch_src[nb] = sst[k];
+        t.batch_dst[nb] = dst_stride[k];
+        nbt *= shape[k];
+        ++nb;
+    }
+    t.nbatch = nb;
+    t.nbatch_total = uint32_t(nbt);
+    int64_t tiles = int64_t(t.tiles_p) * t.tiles_q * nbt;
+    hipLaunchKernelGGL((tile_transpose_kernel<W>), dim3(grid_cap(tiles)), dim3(kThreads), 0, s, t);
+    PE_CHECK_HIP(hipGetLastError());
+    return PE_OK;
+}
+
+}  // namespace
+
+int validate_permute(const pe_permute_desc& d) {
+    if (d.elem_bytes != 2 && d.elem_bytes != 4)
+        return fail(PE_ERR_UNSUPPORTED, "permute: elem_bytes must be 2 or 4");
+    if (d.ndims < 0 || d.ndims > PE_MAX_DIMS) return fail(PE_ERR_INVALID, "permute: ndims out of range");
+    int64_t n = 1, smax = 0;
+    for (int k = 0; k < d.ndims; ++k) {
+        if (d.shape[k] < 0 || d.src_stride[k] < 0)
+            return fail(PE_ERR_INVALID, "permute: negative extent or stride");
+        n *= d.shape[k];
+        if (d.shape[k] > 0) smax += (d.shape[k] - 1) * d.src_stride[k];
+    }
+    if (n > 0 && smax >= d.src_numel)
+        return fail(PE_ERR_BOUNDS, "permute: strides address past the source extent");
+    return PE_OK;
+}
+
+}  // namespace pe
+
+extern "C" int pe_permute(const pe_permute_desc* d, const void* src, void* dst, void* stream) {
+    if (!d) return pe::fail(PE_ERR_INVALID, "permute: null descriptor");
+    int st = pe::validate_permute(*d);
+    if (st != PE_OK) return st;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    return d->elem_bytes == 4 ? pe::run<uint32_t>(*d, src, dst, s) : pe::run<uint16_t>(*d, src, dst, s);
+}

@@ -1,0 +1,334 @@
+// Contraction-free products: Hadamard, broadcast, outer and transposed
+// elementwise einsums, streamed over a row-major float32 output.
+//
+// Reference counterparts: elementwise_mul (pto_einsum_elementwise.h:27-127)
+// and broadcast_mul (pto_einsum_elementwise.h:152-370).  Both are one kernel
+// here: every operand is addressed through per-axis strides (stride 0 where
+// the operand lacks the axis), so the same launch covers the reference's
+// Hadamard, column-expand and scalar broadcast modes and the outer products
+// the reference sends to its matmul path.
+//
+// Numerics follow the reference CPU route (the parity oracle): the Hadamard
+// route stores (float)a*(float)b (cpu_einsum.h:87-92); every other route is a
+// C=1 matmul there and stores 0.0f + (float)a*(float)b (cpu_einsum.h:71-76),
+// which differs from a*b only by turning -0 into +0.  Built with
+// -ffp-contract=off so the multiply and the add round separately, and with
+// denormals preserved.
+//
+// Memory: bandwidth bound (2-3 loads + 1 store per element, no reuse), so the
+// kernel is a grid-stride stream of 16-byte loads and non-temporal 16-byte
+// stores.  Axes are merged on the host first; the innermost merged axis is
+// the vector axis and the outer axes are decoded with multiply-high division.
+#include "pe_common.h"
+
+#include <algorithm>
+#include <vector>
+
+namespace pe {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kMaxOuter = PE_MAX_DIMS - 1;
+
+struct ProductArgs {
+    const void* a;
+    const void* b;
+    float* out;
+    uint32_t nvec;          // vectors in the output (32-bit path)
+    uint32_t inner;         // extent of the innermost axis, in elements
+    FastDiv inner_vecs;     // inner / VEC
+    int32_t nouter;         // outer axes (outermost first)
+    FastDiv outer_div[kMaxOuter];
+    int64_t a_outer[kMaxOuter];
+    int64_t b_outer[kMaxOuter];
+    int64_t a_inner, b_inner;
+};
+
+template <typename E, int VEC>
+struct VecLoad;
+
+template <>
+struct VecLoad<F32, 4> {
+    __device__ __forceinline__ static void load(const float* p, float (&v)[4]) {
+        f32x4 x = *reinterpret_cast<const f32x4*>(p);
+        v[0] = x[0]; v[1] = x[1]; v[2] = x[2]; v[3] = x[3];
+    }
+};
+template <>
+struct VecLoad<F16, 8> {
+    __device__ __forceinline__ static void load(const _Float16* p, float (&v)[8]) {
+        f16x8 x = *reinterpret_cast<const f16x8*>(p);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = (float)x[i];
+    }
+};
+template <typename E>
+struct VecLoad<E, 1> {
+    __device__ __forceinline__ static void load(const typename E::T* p, float (&v)[1]) {
+        v[0] = E::to_f32(*p);
+    }
+};
+
+// B operand per vector: contiguous (B_MODE 1), one broadcast scalar (0) or
+// general per-element stride (2, scalar path only).
+template <typename E, int VEC, int B_MODE>
+__device__ __forceinline__ void load_b(const typename E::T* b, int64_t off, int64_t bstride,
+                                       float (&v)[VEC]) {
+    if constexpr (B_MODE == 1) {
+        VecLoad<E, VEC>::load(b + off, v);
+    } else if constexpr (B_MODE == 0) {
+        float s = E::to_f32(b[off]);
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) v[i] = s;
+    } else {
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) v[i] = E::to_f32(b[off + i * bstride]);
+    }
+}
+
+template <int VEC>
+__device__ __forceinline__ void store_out(float* out, const float (&r)[VEC]) {
+    if constexpr (VEC == 4) {
+        f32x4 v = {r[0], r[1], r[2], r[3]};
+        store_nt(reinterpret_cast<f32x4*>(out), v);
+    } else if constexpr (VEC == 8) {
+        f32x4 v0 = {r[0], r[1], r[2], r[3]};
+        f32x4 v1 = {r[4], r[5], r[6], r[7]};
+        store_nt(reinterpret_cast<f32x4*>(out), v0);
+        store_nt(reinterpret_cast<f32x4*>(out) + 1, v1);
+    } else {
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) store_nt(out + i, r[i]);
+    }
+}
+
+// One launch streams all output vectors.  UNROLL vectors per thread per
+// iteration: all loads are issued before any store so several 16-byte loads
+// are in flight per lane.
+template <typename E, int VEC, int B_MODE, bool ADD_ZERO, bool HAS_OUTER, int UNROLL>
+__global__ __launch_bounds__(kThreads) void product_kernel(ProductArgs p) {
+    using T = typename E::T;
+    const T* __restrict__ a = static_cast<const T*>(p.a);
+    const T* __restrict__ b = static_cast<const T*>(p.b);
+    float* __restrict__ out = p.out;
+    const uint32_t stride = gridDim.x * kThreads;
+    uint32_t v = blockIdx.x * kThreads + threadIdx.x;
+    for (; v < p.nvec; v += stride * UNROLL) {
+        float ra[UNROLL][VEC], rb[UNROLL][VEC];
+        bool live[UNROLL];
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+            uint32_t vv = v + u * stride;
+            live[u] = vv < p.nvec;
+            if (!live[u]) continue;
+            int64_t aoff, boff;
+            if constexpr (HAS_OUTER) {
+                uint32_t row, colv;
+                p.inner_vecs.divmod(vv, row, colv);
+                uint32_t col = colv * VEC;
+                aoff = int64_t(col) * p.a_inner;
+                boff = int64_t(col) * p.b_inner;
+                for (int d = p.nouter - 1; d >= 0; --d) {
+                    uint32_t q, r;
+                    p.outer_div[d].divmod(row, q, r);
+                    aoff += int64_t(r) * p.a_outer[d];
+                    boff += int64_t(r) * p.b_outer[d];
+                    row = q;
+                }
+            } else {
+                aoff = int64_t(vv) * VEC * p.a_inner;
+                boff = int64_t(vv) * VEC * p.b_inner;
+            }
+            if constexpr (VEC > 1) {
+                VecLoad<E, VEC>::load(a + aoff, ra[u]);
+            } else {
+                ra[u][0] = E::to_f32(a[aoff]);
+            }
+            load_b<E, VEC, B_MODE>(b, boff, p.b_inner, rb[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+            if (!live[u]) continue;
+            float r[VEC];
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) {
+                float prod = ra[u][i] * rb[u][i];
+                r[i] = ADD_ZERO ? 0.0f + prod : prod;
+            }
+            store_out<VEC>(out + int64_t(v + u * stride) * VEC, r);
+        }
+    }
+}
+
+// Fallback for outputs of 2^31 elements or more: 64-bit division per element.
+template <typename E, bool ADD_ZERO>
+__global__ __launch_bounds__(kThreads) void product_kernel_wide(
+    const typename E::T* __restrict__ a, const typename E::T* __restrict__ b,
+    float* __restrict__ out, int64_t n, int32_t ndims, pe_product_desc d) {
+    const int64_t stride = int64_t(gridDim.x) * kThreads;
+    for (int64_t o = int64_t(blockIdx.x) * kThreads + threadIdx.x; o < n; o += stride) {
+        int64_t rem = o, aoff = 0, boff = 0;
+        for (int k = ndims - 1; k >= 0; --k) {
+            int64_t x = rem % d.shape[k];
+            rem /= d.shape[k];
+            aoff += x * d.a_stride[k];
+            boff += x * d.b_stride[k];
+        }
+        float prod = E::to_f32(a[aoff]) * E::to_f32(b[boff]);
+        store_nt(out + o, ADD_ZERO ? 0.0f + prod : prod);
+    }
+}
+
+// Merge adjacent output axes whose strides compose in both operands
+// (stride[d] == extent[d+1] * stride[d+1]), dropping extent-1 axes.
+void merge_axes(const pe_product_desc& d, std::vector<int64_t>& shape,
+                std::vector<int64_t>& sa, std::vector<int64_t>& sb) {
+    shape.clear(); sa.clear(); sb.clear();
+    for (int k = 0; k < d.ndims; ++k) {
+        if (d.shape[k] == 1) continue;
+        if (!shape.empty() && sa.back() == d.shape[k] * d.a_stride[k] &&
+            sb.back() == d.shape[k] * d.b_stride[k]) {
+            shape.back() *= d.shape[k];
+            sa.back() = d.a_stride[k];
+            sb.back() = d.b_stride[k];
+        } else {
+            shape.push_back(d.shape[k]);
+            sa.push_back(d.a_stride[k]);
+            sb.push_back(d.b_stride[k]);
+        }
+    }
+}
+
+int grid_for(int64_t work_items, int per_block) {
+    int64_t blocks = ceil_div(std::max<int64_t>(work_items, 1), per_block);
+    int64_t cap = int64_t(cu_count()) * 16;  // enough resident waves to cover HBM latency
+    return int(std::max<int64_t>(1, std::min(blocks, cap)));
+}
+
+template <typename E, int VEC, int B_MODE, bool ADD_ZERO, bool HAS_OUTER>
+hipError_t launch_vec(const ProductArgs& args, hipStream_t s) {
+    constexpr int U = (VEC >= 4) ? 2 : 4;
+    int grid = grid_for(ceil_div(args.nvec, U), kThreads);
+    hipLaunchKernelGGL((product_kernel<E, VEC, B_MODE, ADD_ZERO, HAS_OUTER, U>), dim3(grid),
+                       dim3(kThreads), 0, s, args);
+    return hipGetLastError();
+}
+
+template <typename E, int VEC, bool ADD_ZERO, bool HAS_OUTER>
+hipError_t launch_bmode(const ProductArgs& args, int bmode, hipStream_t s) {
+    if (bmode == 1) return launch_vec<E, VEC, 1, ADD_ZERO, HAS_OUTER>(args, s);
+    if (bmode == 0) return launch_vec<E, VEC, 0, ADD_ZERO, HAS_OUTER>(args, s);
+    return launch_vec<E, 1, 2, ADD_ZERO, HAS_OUTER>(args, s);
+}
+
+template <typename E>
+int run(const pe_product_desc& d, const void* in0, const void* in1, float* out,
+        hipStream_t s) {
+    using T = typename E::T;
+    std::vector<int64_t> shape, sa, sb;
+    merge_axes(d, shape, sa, sb);
+    int64_t n = 1;
+    for (int64_t x : shape) n *= x;
+    if (n == 0) return PE_OK;
+    const bool add_zero = d.add_zero != 0;
+
+    if (n >= (int64_t(1) << 31) || int(shape.size()) > kMaxOuter + 1) {
+        pe_product_desc m = d;
+        m.ndims = int32_t(shape.size());
+        for (size_t k = 0; k < shape.size(); ++k) {
+            m.shape[k] = shape[k]; m.a_stride[k] = sa[k]; m.b_stride[k] = sb[k];
+        }
+        int grid = grid_for(n, kThreads);
+        if (add_zero)
+            hipLaunchKernelGGL((product_kernel_wide<E, true>), dim3(grid), dim3(kThreads), 0, s,
+                               (const T*)in0, (const T*)in1, out, n, m.ndims, m);
+        else
+            hipLaunchKernelGGL((product_kernel_wide<E, false>), dim3(grid), dim3(kThreads), 0, s,
+                               (const T*)in0, (const T*)in1, out, n, m.ndims, m);
+        PE_CHECK_HIP(hipGetLastError());
+        return PE_OK;
+    }
+
+    ProductArgs args{};
+    args.a = in0; args.b = in1; args.out = out;
+    const int nd = int(shape.size());
+    const int64_t inner = nd ? shape[nd - 1] : 1;
+    args.inner = uint32_t(inner);
+    args.a_inner = nd ? sa[nd - 1] : 0;
+    args.b_inner = nd ? sb[nd - 1] : 0;
+    args.nouter = std::max(0, nd - 1);
+    for (int k = 0; k < args.nouter; ++k) {
+        args.outer_div[k].init(uint32_t(shape[k]));
+        args.a_outer[k] = sa[k];
+        args.b_outer[k] = sb[k];
+    }
+
+    // Vector path: 16-byte loads of in0 along the innermost axis.  Needs a
+    // unit inner stride, an inner extent and outer strides that are whole
+    // vectors, and vector-aligned base pointers.
+    constexpr int VEC = 16 / E::kBytes;
+    bool vec_ok = nd > 0 && args.a_inner == 1 && (args.b_inner == 0 || args.b_inner == 1) &&
+                  inner % VEC == 0 && aligned(in0, 16) && aligned(out, 16) &&
+                  (args.b_inner == 0 || aligned(in1, 16));
+    for (int k = 0; k < args.nouter && vec_ok; ++k)
+        vec_ok = (sa[k] % VEC == 0) && (args.b_inner == 0 || sb[k] % VEC == 0);
+    const bool has_outer = args.nouter > 0;
+
+    hipError_t e;
+    if (vec_ok) {
+        args.nvec = uint32_t(n / VEC);
+        args.inner_vecs.init(uint32_t(inner / VEC));
+        int bmode = args.b_inner == 1 ? 1 : 0;
+        if (add_zero)
+            e = has_outer ? launch_bmode<E, VEC, true, true>(args, bmode, s)
+                          : launch_bmode<E, VEC, true, false>(args, bmode, s);
+        else
+            e = has_outer ? launch_bmode<E, VEC, false, true>(args, bmode, s)
+                          : launch_bmode<E, VEC, false, false>(args, bmode, s);
+    } else {
+        args.nvec = uint32_t(n);
+        args.inner_vecs.init(uint32_t(inner));
+        if (add_zero)
+            e = has_outer ? launch_bmode<E, 1, true, true>(args, 2, s)
+                          : launch_bmode<E, 1, true, false>(args, 2, s);
+        else
+            e = has_outer ? launch_bmode<E, 1, false, true>(args, 2, s)
+                          : launch_bmode<E, 1, false, false>(args, 2, s);
+    }
+    PE_CHECK_HIP(e);
+    return PE_OK;
+}
+
+}  // namespace
+
+int validate_product(const pe_product_desc& d) {
+    if (d.dtype != PE_F32 && d.dtype != PE_F16)
+        return fail(PE_ERR_UNSUPPORTED, "product: dtype must be PE_F32 or PE_F16");
+    if (d.ndims < 0 || d.ndims > PE_MAX_DIMS)
+        return fail(PE_ERR_INVALID, "product: ndims out of range");
+    int64_t amax = 0, bmax = 0, n = 1;
+    for (int k = 0; k < d.ndims; ++k) {
+        if (d.shape[k] < 0 || d.a_stride[k] < 0 || d.b_stride[k] < 0)
+            return fail(PE_ERR_INVALID, "product: negative extent or stride");
+        n *= d.shape[k];
+        if (d.shape[k] > 0) {
+            amax += (d.shape[k] - 1) * d.a_stride[k];
+            bmax += (d.shape[k] - 1) * d.b_stride[k];
+        }
+    }
+    if (n > 0 && (amax >= d.a_numel || bmax >= d.b_numel))
+        return fail(PE_ERR_BOUNDS, "product: strides address past an operand's extent");
+    return PE_OK;
+}
+
+}  // namespace pe
+
+extern "C" int pe_product(const pe_product_desc* d, const void* in0, const void* in1,
+                          float* out, void* stream) {
+    if (!d) return pe::fail(PE_ERR_INVALID, "product: null descriptor");
+    int st = pe::validate_product(*d);
+    if (st != PE_OK) return st;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    return d->dtype == PE_F32 ? pe::run<pe::F32>(*d, in0, in1, out, s)
+                              : pe::run<pe::F16>(*d, in0, in1, out, s);
+}

@@ -1,0 +1,17 @@
+"""pto_einsum for AMD Instinct MI355X (gfx950).
+
+Public API, unchanged from the reference (src/pto_einsum/__init__.py:12-15):
+
+    einsum(equation, a, b, device="cuda")   -> float32 result tensor
+    EinsumBuilder(equation, shapes, dtype)  -> reusable compiled runner
+    INCLUDE_DIR                             -> headers the JIT sources compile against
+
+Example:
+    >>> from pto_einsum import einsum
+    >>> c = einsum("ij, jk -> ik", a, b)    # a, b are tensors on the GPU
+"""
+
+from .builder import EinsumBuilder, INCLUDE_DIR, einsum
+
+__all__ = ["einsum", "EinsumBuilder", "INCLUDE_DIR"]
+__version__ = "0.1.0"

@@ -1,0 +1,290 @@
+"""MI355X launch plan: turn an einsum recipe into kernel descriptors.
+
+The reference executes every contraction as Phase A (operand transposes into
+``[I, L0, C]`` / ``[I, C, L1]``), Phase B (GEMM) and Phase C (output
+transpose), dropping A or C only for a fixed set of read / store modes
+(builder.py:263-346).  Here the GEMM reads each operand at its own strides,
+so a phase is only kept when an axis group genuinely does not collapse:
+
+* every role group (free0 = M, free1 = N, contract = K) is flattened to one
+  (extent, stride) pair in each tensor that carries it, trying axis orders
+  that follow the memory layout;
+* batch (inplace) axes stay separate, each with its own stride per tensor;
+* a tensor in which some group cannot be flattened is staged in the
+  canonical recipe layout -- the operand gathered into the workspace
+  (Phase A) or the result written there and permuted into the output
+  (Phase C) -- and groups touching a staged tensor use the recipe's axis
+  order everywhere.
+
+Contraction-free equations whose every output is a single product (C == 1)
+take the product route: one strided stream kernel.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from math import prod
+from typing import Dict, List, Optional, Sequence, Tuple
+
+from .planner import row_major_strides, split_equation, transpose_config
+
+ROUTE_PRODUCT = 0
+ROUTE_GEMM = 1
+MAX_DIMS = 8
+DT_F32, DT_F16 = 0, 1
+
+
+@dataclass
+class ProductDesc:
+    dtype: int
+    add_zero: int
+    shape: List[int]
+    a_stride: List[int]
+    b_stride: List[int]
+    a_numel: int
+    b_numel: int
+
+
+@dataclass
+class PermuteDesc:
+    elem_bytes: int
+    shape: List[int]
+    src_stride: List[int]
+    src_numel: int
+
+
+@dataclass
+class GemmDesc:
+    dtype: int
+    batch_shape: List[int]
+    a_bstride: List[int]
+    b_bstride: List[int]
+    c_bstride: List[int]
+    M: int
+    N: int
+    K: int
+    a_ms: int
+    a_ks: int
+    b_ks: int
+    b_ns: int
+    c_ms: int
+    c_ns: int
+    a_numel: int
+    b_numel: int
+    c_numel: int
+    split_k: int = 0
+    tile: int = 0
+
+
+@dataclass
+class LaunchPlan:
+    route: int
+    product: Optional[ProductDesc] = None
+    gemm: Optional[GemmDesc] = None
+    gather0: bool = False
+    gather1: bool = False
+    scatter_out: bool = False
+    perm0: Optional[PermuteDesc] = None
+    perm1: Optional[PermuteDesc] = None
+    perm_out: Optional[PermuteDesc] = None
+    ws0_off: int = 0
+    ws1_off: int = 0
+    wsout_off: int = 0
+    ws_bytes: int = 0
+    # Component descriptors (run_transpose_inp0/inp1/out, run_batched_matmul).
+    comp_perm0: Optional[PermuteDesc] = None
+    comp_perm1: Optional[PermuteDesc] = None
+    comp_perm_out: Optional[PermuteDesc] = None
+    comp_gemm: Optional[GemmDesc] = None
+    notes: Dict[str, str] = field(default_factory=dict)
+
+
+def _align(x: int, a: int = 256) -> int:
+    return (x + a - 1) // a * a
+
+
+def _permute_desc(shape, perm, elem_bytes) -> PermuteDesc:
+    cfg = transpose_config("p", shape, perm)
+    return PermuteDesc(elem_bytes, list(cfg["to_shape"]), list(cfg["perm_strides"]),
+                       max(1, cfg["N"]))
+
+
+def _mergeable(order: Sequence[str], size: Dict[str, int], stride: Dict[str, int]) -> bool:
+    """True when axes ``order`` (outermost first) address like one axis."""
+    axes = [a for a in order if size[a] != 1]
+    for x, y in zip(axes, axes[1:]):
+        if stride[x] != size[y] * stride[y]:
+            return False
+    return True
+
+
+def _inner_stride(order: Sequence[str], size: Dict[str, int], stride: Dict[str, int]) -> int:
+    axes = [a for a in order if size[a] != 1]
+    return stride[axes[-1]] if axes else 0
+
+
+def _candidate_orders(group: Sequence[str], size, strides: Sequence[Dict[str, int]]):
+    seen = []
+    for st in strides:
+        order = tuple(sorted(group, key=lambda a: (-st[a], group.index(a))))
+        if order not in seen:
+            seen.append(order)
+    if tuple(group) not in seen:
+        seen.append(tuple(group))
+    return seen
+
+
+def _component_descs(plan: LaunchPlan, recipe: Dict, shape0, shape1, dtype_code: int, elem: int):
+    """Descriptors of the staged component entry points: the operand
+    permutations into ``[I, L0, C]`` / ``[I, C, L1]``, the canonical batched
+    GEMM and the output permutation (reference: templates.py:166-177)."""
+    I, L0, L1, C = recipe["I"], recipe["L0"], recipe["L1"], recipe["C"]
+    perm0, perm1 = recipe["in_transpose_idxs"]
+    plan.comp_perm0 = _permute_desc(shape0, perm0, elem)
+    plan.comp_perm1 = _permute_desc(shape1, perm1, elem)
+    plan.comp_perm_out = _permute_desc(tuple(recipe["out_interpret_shape"]),
+                                       recipe["out_transpose_idxs"], 4)
+    batched = I != 1
+    plan.comp_gemm = GemmDesc(
+        dtype=dtype_code, batch_shape=[I] if batched else [],
+        a_bstride=[L0 * C] if batched else [], b_bstride=[C * L1] if batched else [],
+        c_bstride=[L0 * L1] if batched else [],
+        M=L0, N=L1, K=C, a_ms=C, a_ks=1, b_ks=L1, b_ns=1, c_ms=L1, c_ns=1,
+        a_numel=max(1, I * L0 * C), b_numel=max(1, I * C * L1), c_numel=max(1, I * L0 * L1),
+        split_k=1)
+
+
+def plan_launch(recipe: Dict, exec_eq: str, shape0, shape1, dtype_code: int) -> LaunchPlan:
+    """Build the launch plan for ``exec_eq`` on operands of ``shape0``/``shape1``
+    (already in execution order, i.e. after any operand swap)."""
+    t0, t1, to = split_equation(exec_eq)
+    shape0, shape1 = tuple(int(s) for s in shape0), tuple(int(s) for s in shape1)
+    out_shape = tuple(recipe["out_shape"])
+    elem = 4 if dtype_code == DT_F32 else 2
+    size: Dict[str, int] = {}
+    for t, s in ((t0, shape0), (t1, shape1)):
+        size.update({a: int(n) for a, n in zip(t, s)})
+    st0 = dict(zip(t0, row_major_strides(shape0)))
+    st1 = dict(zip(t1, row_major_strides(shape1)))
+    sto = dict(zip(to, row_major_strides(out_shape)))
+    numel0, numel1, numelo = max(1, prod(shape0)), max(1, prod(shape1)), max(1, prod(out_shape))
+
+    contract_set = set(t0) & set(t1) - set(to)
+    C = prod(size[a] for a in contract_set)
+    if C == 1:
+        prod_desc = ProductDesc(
+            dtype=dtype_code,
+            add_zero=0 if recipe["elementwise"] else 1,
+            shape=list(out_shape),
+            a_stride=[st0.get(a, 0) for a in to],
+            b_stride=[st1.get(a, 0) for a in to],
+            a_numel=numel0, b_numel=numel1)
+        # Drop extent-1 axes so the rank fits the descriptor.
+        keep = [i for i, n in enumerate(out_shape) if n != 1]
+        prod_desc.shape = [out_shape[i] for i in keep]
+        prod_desc.a_stride = [prod_desc.a_stride[i] for i in keep]
+        prod_desc.b_stride = [prod_desc.b_stride[i] for i in keep]
+        if len(keep) > MAX_DIMS:
+            raise ValueError(f"einsum '{exec_eq}': more than {MAX_DIMS} non-unit output axes")
+        plan = LaunchPlan(route=ROUTE_PRODUCT, product=prod_desc)
+        if not recipe["elementwise"] and not recipe["broadcast"]:
+            _component_descs(plan, recipe, shape0, shape1, dtype_code, elem)
+        return plan
+
+    roles = recipe["roles"]
+    batch = [a for a in roles["inplace"]]
+    mgrp = list(roles["invariant0"])
+    ngrp = list(roles["invariant1"])
+    kgrp = list(roles["contract"])
+    I, L0, L1 = prod(size[a] for a in batch), prod(size[a] for a in mgrp), prod(size[a] for a in ngrp)
+
+    # Canonical (recipe-order) layouts used when a tensor is staged.
+    can0 = dict(zip(batch + mgrp + kgrp, row_major_strides([size[a] for a in batch + mgrp + kgrp])))
+    can1 = dict(zip(batch + kgrp + ngrp, row_major_strides([size[a] for a in batch + kgrp + ngrp])))
+    cano = dict(zip(batch + mgrp + ngrp, row_major_strides([size[a] for a in batch + mgrp + ngrp])))
+
+    staged = {"A": False, "B": False, "C": False}
+
+    def strides_of(t):
+        if t == "A":
+            return can0 if staged["A"] else st0
+        if t == "B":
+            return can1 if staged["B"] else st1
+        return cano if staged["C"] else sto
+
+    groups = (("M", mgrp, ("A", "C")), ("N", ngrp, ("B", "C")), ("K", kgrp, ("A", "B")))
+    orders: Dict[str, Tuple[str, ...]] = {}
+    for _ in range(4):
+        changed = False
+        for name, grp, tensors in groups:
+            if any(staged[t] for t in tensors):
+                order = tuple(grp)
+                for t in tensors:
+                    if not staged[t] and not _mergeable(order, size, strides_of(t)):
+                        staged[t] = True
+                        changed = True
+            else:
+                order = None
+                for cand in _candidate_orders(grp, size, [strides_of(t) for t in tensors]):
+                    if all(_mergeable(cand, size, strides_of(t)) for t in tensors):
+                        order = cand
+                        break
+                if order is None:
+                    order = tuple(grp)
+                    for t in tensors:
+                        if not _mergeable(order, size, strides_of(t)):
+                            staged[t] = True
+                            changed = True
+            orders[name] = order
+        if not changed:
+            break
+
+    sA, sB, sC = strides_of("A"), strides_of("B"), strides_of("C")
+    # Batch axes in output order, extent-1 axes dropped, adjacent axes merged
+    # when they compose in all three tensors.
+    bax = [a for a in sorted(batch, key=to.index) if size[a] != 1]
+    bshape, ba, bb, bc = [], [], [], []
+    for a in bax:
+        if bshape and ba[-1] == size[a] * sA[a] and bb[-1] == size[a] * sB[a] and bc[-1] == size[a] * sC[a]:
+            bshape[-1] *= size[a]
+            ba[-1], bb[-1], bc[-1] = sA[a], sB[a], sC[a]
+        else:
+            bshape.append(size[a])
+            ba.append(sA[a])
+            bb.append(sB[a])
+            bc.append(sC[a])
+    if len(bshape) > MAX_DIMS:
+        raise ValueError(f"einsum '{exec_eq}': more than {MAX_DIMS} independent batch axes")
+
+    gemm = GemmDesc(
+        dtype=dtype_code, batch_shape=bshape, a_bstride=ba, b_bstride=bb, c_bstride=bc,
+        M=L0, N=L1, K=C,
+        a_ms=_inner_stride(orders["M"], size, sA), a_ks=_inner_stride(orders["K"], size, sA),
+        b_ks=_inner_stride(orders["K"], size, sB), b_ns=_inner_stride(orders["N"], size, sB),
+        c_ms=_inner_stride(orders["M"], size, sC), c_ns=_inner_stride(orders["N"], size, sC),
+        a_numel=numel0, b_numel=numel1, c_numel=numelo)
+
+    plan = LaunchPlan(route=ROUTE_GEMM, gemm=gemm, gather0=staged["A"], gather1=staged["B"],
+                      scatter_out=staged["C"])
+    _component_descs(plan, recipe, shape0, shape1, dtype_code, elem)
+
+    off = 0
+    if plan.gather0:
+        plan.perm0 = plan.comp_perm0
+        plan.ws0_off = off
+        off = _align(off + numel0 * elem)
+    if plan.gather1:
+        plan.perm1 = plan.comp_perm1
+        plan.ws1_off = off
+        off = _align(off + numel1 * elem)
+    if plan.scatter_out:
+        plan.perm_out = plan.comp_perm_out
+        plan.wsout_off = off
+        off = _align(off + numelo * 4)
+    plan.ws_bytes = off
+    if plan.gather0:
+        gemm.a_numel = numel0
+    if plan.scatter_out:
+        gemm.c_numel = numelo
+    plan.notes = dict(M_order="".join(orders["M"]), N_order="".join(orders["N"]),
+                      K_order="".join(orders["K"]))
+    return plan

@@ -1,0 +1,144 @@
+"""GPU parity: the gfx950 path against the CPU oracle, through the public API.
+
+Case lists follow the reference's own test matrices (tests/test_einsum.py:22-129,
+tests/test_llm_ops.py:34-125) plus the BASELINE equations at reduced sizes and
+edge shapes.  Every case runs in float32 and float16.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from parity_util import RTOL, check, contraction_size, make_inputs
+from ref_cases import ATTENTION_CASES, BROADCAST_CASES, CHAIN_CASES, CONFIG_CASES, EINSUM_CASES
+
+pytestmark = pytest.mark.gpu
+
+ALL_CASES = EINSUM_CASES + ATTENTION_CASES + BROADCAST_CASES + CHAIN_CASES + CONFIG_CASES
+
+
+def _id(c):
+    eq, s0, s1 = c
+    return f"{eq}-{'x'.join(map(str, s0))}-{'x'.join(map(str, s1))}"
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16], ids=["f32", "f16"])
+@pytest.mark.parametrize("eq,s0,s1", ALL_CASES, ids=[_id(c) for c in ALL_CASES])
+def test_parity(eq, s0, s1, dtype, build_dir):
+    from pto_einsum import einsum
+
+    a, b = make_inputs(eq, s0, s1, dtype)
+    got = einsum(eq, a.cuda(), b.cuda()).cpu().numpy()
+    want = oracle.einsum(eq, a.float().numpy(), b.float().numpy())
+    exact = contraction_size(eq, s0, s1) <= 1
+    check(got, want, exact, RTOL[dtype], f"{eq} {s0} {s1} {dtype}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16], ids=["f32", "f16"])
+@pytest.mark.parametrize("eq,s0,s1", [
+    ("bij,bjk->bik", (64, 128, 128), (64, 128, 128)),       # test_einsum.py:244-272
+    ("bihd,bjhd->bihj", (2, 128, 16, 128), (2, 128, 16, 128)),  # :275-304 (NT)
+    ("bihj,bjhd->bihd", (2, 128, 16, 128), (2, 128, 16, 128)),  # :307-334 (NN-strided)
+    ("bvhd,bvhe->bhde", (2, 128, 16, 128), (2, 128, 16, 128)),  # :337-364 (TN)
+    ("ts,sp->tp", (512, 2048), (2048, 64)),                     # split-K reduction
+])
+def test_deterministic(eq, s0, s1, dtype, build_dir):
+    """Eight more runs on the same inputs are bit-identical to the first."""
+    from pto_einsum import EinsumBuilder
+
+    builder = EinsumBuilder(eq, [s0, s1], dtype)
+    run = builder.build()
+    a, b = make_inputs(eq, s0, s1, dtype)
+    a, b = a.cuda(), b.cuda()
+    ref = run(a, b).clone()
+    want = oracle.einsum(eq, a.float().cpu().numpy(), b.float().cpu().numpy())
+    check(ref.cpu().numpy(), want, False, RTOL[dtype], eq)
+    for _ in range(8):
+        assert torch.equal(run(a, b), ref), f"{eq}: run-to-run difference"
+    builder.cleanup()
+
+
+def test_builder_reuse(build_dir):
+    """test_einsum.py:208-241: a runner reused with fresh data, incl. K != C."""
+    from pto_einsum import EinsumBuilder
+
+    for eq, s0, s1, reps in (("ij,jk->ik", (32, 64), (64, 32), 3),
+                             ("bij,bjk->bik", (8, 16, 20), (8, 20, 64), 10)):
+        run = EinsumBuilder(eq, [s0, s1], torch.float32).build()
+        g = torch.Generator().manual_seed(7)
+        for _ in range(reps):
+            a, b = torch.rand(s0, generator=g), torch.rand(s1, generator=g)
+            got = run(a.cuda(), b.cuda()).cpu().numpy()
+            check(got, oracle.einsum(eq, a.numpy(), b.numpy()), False, 1e-4, eq)
+
+
+def test_special_values_bit_exact(build_dir):
+    """Hadamard and broadcast keep subnormals, signed zeros, inf and NaN
+    exactly as the oracle does (Hadamard: a*b; broadcast route: 0 + a*b)."""
+    from pto_einsum import einsum
+
+    specials = np.array([0.0, -0.0, 1e-40, -1e-40, 1.17549435e-38, 3.4e38, -3.4e38,
+                         np.inf, -np.inf, 1.0, -1.0, 0.5, 2.0, 1e-20, -1e-20, 7.0], dtype=np.float32)
+    a = np.tile(specials, 16)
+    b = np.repeat(specials, 16)
+    ta, tb = torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda()
+    got = einsum("i,i->i", ta, tb).cpu().numpy()
+    want = oracle.einsum("i,i->i", a, b)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    check(np.where(nan, 0, got).astype(np.float32), np.where(nan, 0, want).astype(np.float32), True, 0, "hadamard")
+    a2 = a.reshape(16, 16)
+    got2 = einsum("ij,j->ij", torch.from_numpy(a2).cuda(), torch.from_numpy(specials).cuda()).cpu().numpy()
+    want2 = oracle.einsum("ij,j->ij", a2, specials)
+    nan2 = np.isnan(want2)
+    assert np.array_equal(np.isnan(got2), nan2)
+    check(np.where(nan2, 0, got2).astype(np.float32), np.where(nan2, 0, want2).astype(np.float32), True, 0, "bcast")
+
+
+def test_decay_mask_subnormals(build_dir):
+    """Config-4a shape family at a reduced size: with gamma = 0.96 the decay
+    0.96^(t-s) falls below FLT_MIN inside a 2048 window, so the products
+    cover normals, subnormals and underflow to zero."""
+    from pto_einsum import einsum
+
+    t = 2048
+    g = torch.Generator().manual_seed(3)
+    x = torch.rand(t, t, generator=g)
+    i = torch.arange(t, dtype=torch.float64)
+    m = torch.where(i[:, None] >= i[None, :], 0.96 ** (i[:, None] - i[None, :]), torch.zeros(())).float()
+    got = einsum("ts,ts->ts", x.cuda(), m.cuda()).cpu().numpy()
+    want = oracle.hadamard(x.numpy(), m.numpy())
+    assert np.count_nonzero((want != 0) & (np.abs(want) < 1.17549435e-38)) > 0
+    check(got, want, True, 0, "decay mask")
+
+
+def test_validation_errors(build_dir):
+    """test_einsum.py:400-425 contracts on the GPU device."""
+    from pto_einsum import EinsumBuilder, einsum
+
+    a = torch.rand(32, 64, device="cuda")
+    b = torch.rand(64, 32, device="cuda")
+    with pytest.raises(ValueError, match="Only exactly two operands are supported."):
+        einsum("ij,jk->ik", a)
+    with pytest.raises(ValueError, match="Operands must have the same datatype."):
+        einsum("ij,jk->ik", a, b.to(torch.int32))
+    run = EinsumBuilder("ij,jk->ik", [(32, 64), (64, 32)], torch.float32).build()
+    with pytest.raises(ValueError, match="do not match built shapes"):
+        run(torch.rand(32, 32, device="cuda"), b)
+    with pytest.raises(TypeError, match="do not match built datatype"):
+        run(a, b.to(torch.int32))
+    with pytest.raises(ValueError, match="single-operand reduction is not supported"):
+        einsum("ij,jk->k", a, b)
+    with pytest.raises(TypeError, match="Unsupported torch dtype"):
+        einsum("ij,jk->ik", a.bfloat16(), b.bfloat16())
+
+
+def test_non_contiguous_and_npu_alias(build_dir):
+    from pto_einsum import einsum
+
+    g = torch.Generator().manual_seed(11)
+    base = torch.rand(64, 96, generator=g)
+    b = torch.rand(64, 40, generator=g)
+    at = base.cuda().t()  # non-contiguous view (96, 64)
+    got = einsum("ij,jk->ik", at, b.cuda(), device="npu").cpu().numpy()
+    check(got, oracle.einsum("ij,jk->ik", base.t().contiguous().numpy(), b.numpy()), False, 1e-4, "view")
