@@ -197,46 +197,67 @@ def plan_launch(recipe: Dict, exec_eq: str, shape0, shape1, dtype_code: int) -> 
     kgrp = list(roles["contract"])
     I, L0, L1 = prod(size[a] for a in batch), prod(size[a] for a in mgrp), prod(size[a] for a in ngrp)
 
-    # Canonical (recipe-order) layouts used when a tensor is staged.
-    can0 = dict(zip(batch + mgrp + kgrp, row_major_strides([size[a] for a in batch + mgrp + kgrp])))
-    can1 = dict(zip(batch + kgrp + ngrp, row_major_strides([size[a] for a in batch + kgrp + ngrp])))
-    cano = dict(zip(batch + mgrp + ngrp, row_major_strides([size[a] for a in batch + mgrp + ngrp])))
-
+    # Staging: a tensor in which some axis group does not collapse is staged
+    # in the workspace with its groups contiguous -- [batch, M, K] for A,
+    # [batch, K, N] for B, [batch, M, N] for C -- and each group in the order
+    # its unstaged partner tensor wants, so only the offending tensor moves.
+    natural = {"A": st0, "B": st1, "C": sto}
     staged = {"A": False, "B": False, "C": False}
-
-    def strides_of(t):
-        if t == "A":
-            return can0 if staged["A"] else st0
-        if t == "B":
-            return can1 if staged["B"] else st1
-        return cano if staged["C"] else sto
-
     groups = (("M", mgrp, ("A", "C")), ("N", ngrp, ("B", "C")), ("K", kgrp, ("A", "B")))
+
+    def own_order(grp, t):
+        """An axis order in which ``grp`` collapses in unstaged tensor t, or None."""
+        for cand in _candidate_orders(grp, size, [natural[t]]):
+            if _mergeable(cand, size, natural[t]):
+                return cand
+        return None
+
     orders: Dict[str, Tuple[str, ...]] = {}
     for _ in range(4):
         changed = False
-        for name, grp, tensors in groups:
-            if any(staged[t] for t in tensors):
-                order = tuple(grp)
-                for t in tensors:
-                    if not staged[t] and not _mergeable(order, size, strides_of(t)):
-                        staged[t] = True
-                        changed = True
-            else:
-                order = None
-                for cand in _candidate_orders(grp, size, [strides_of(t) for t in tensors]):
-                    if all(_mergeable(cand, size, strides_of(t)) for t in tensors):
+        for name, grp, (t1, t2) in groups:
+            live = [t for t in (t1, t2) if not staged[t]]
+            order = None
+            if len(live) == 2:
+                for cand in _candidate_orders(grp, size, [natural[t1], natural[t2]]):
+                    if _mergeable(cand, size, natural[t1]) and _mergeable(cand, size, natural[t2]):
                         order = cand
                         break
                 if order is None:
+                    # Keep the tensor that can hold the group by itself; stage the
+                    # other (output last: staging C costs a full extra pass).
+                    keep = t2 if (t2 == "C" or own_order(grp, t1) is None) and own_order(grp, t2) else t1
+                    drop = t1 if keep == t2 else t2
+                    staged[drop] = True
+                    changed = True
+                    order = own_order(grp, keep)
+                    if order is None:
+                        staged[keep] = True
+                        order = tuple(grp)
+            elif len(live) == 1:
+                order = own_order(grp, live[0])
+                if order is None:
+                    staged[live[0]] = True
+                    changed = True
                     order = tuple(grp)
-                    for t in tensors:
-                        if not _mergeable(order, size, strides_of(t)):
-                            staged[t] = True
-                            changed = True
+            else:
+                order = tuple(grp)
             orders[name] = order
         if not changed:
             break
+
+    border = sorted(batch, key=to.index)
+
+    def staged_strides(layout):
+        axes = [a for part in layout for a in part]
+        return dict(zip(axes, row_major_strides([size[a] for a in axes])))
+
+    layouts = {"A": (border, orders["M"], orders["K"]), "B": (border, orders["K"], orders["N"]),
+               "C": (border, orders["M"], orders["N"])}
+    stage_st = {t: staged_strides(layouts[t]) for t in layouts}
+
+    def strides_of(t):
+        return stage_st[t] if staged[t] else natural[t]
 
     sA, sB, sC = strides_of("A"), strides_of("B"), strides_of("C")
     # Batch axes in output order, extent-1 axes dropped, adjacent axes merged
@@ -267,24 +288,26 @@ def plan_launch(recipe: Dict, exec_eq: str, shape0, shape1, dtype_code: int) -> 
                       scatter_out=staged["C"])
     _component_descs(plan, recipe, shape0, shape1, dtype_code, elem)
 
+    def gather_desc(t, src_strides, eb):
+        axes = [a for part in layouts[t] for a in part]
+        return PermuteDesc(eb, [size[a] for a in axes], [src_strides[a] for a in axes],
+                           max(1, prod(size[a] for a in src_strides)))
+
     off = 0
     if plan.gather0:
-        plan.perm0 = plan.comp_perm0
+        plan.perm0 = gather_desc("A", st0, elem)
         plan.ws0_off = off
         off = _align(off + numel0 * elem)
     if plan.gather1:
-        plan.perm1 = plan.comp_perm1
+        plan.perm1 = gather_desc("B", st1, elem)
         plan.ws1_off = off
         off = _align(off + numel1 * elem)
     if plan.scatter_out:
-        plan.perm_out = plan.comp_perm_out
+        cst = stage_st["C"]
+        plan.perm_out = PermuteDesc(4, list(out_shape), [cst[a] for a in to], numelo)
         plan.wsout_off = off
         off = _align(off + numelo * 4)
     plan.ws_bytes = off
-    if plan.gather0:
-        gemm.a_numel = numel0
-    if plan.scatter_out:
-        gemm.c_numel = numelo
     plan.notes = dict(M_order="".join(orders["M"]), N_order="".join(orders["N"]),
                       K_order="".join(orders["K"]))
     return plan

@@ -56,3 +56,17 @@ def check(got: np.ndarray, want: np.ndarray, exact: bool, rtol: float, what: str
     err = np.abs(got.astype(np.float64) - want.astype(np.float64))
     worst = float(err.max()) if err.size else 0.0
     assert worst <= atol, f"{what}: max abs err {worst:.3e} > {atol:.3e} (rtol {rtol} x max|oracle| {scale:.3e})"
+
+
+def ref64_gpu(eq, a, b):
+    """float64 reference on the GPU: operands permuted into contiguous
+    [I, L0, C] / [I, C, L1] blocks (the CPU route's recipe), one batched
+    matmul, then the output permutation.  Avoids torch.einsum's internal
+    transposed views."""
+    r, swapped = oracle.cpu_plan(eq, tuple(a.shape), tuple(b.shape))
+    if swapped:
+        a, b = b, a
+    a = a.cuda().double().permute(r["perm0"]).contiguous().reshape(r["I"], r["L0"], r["C"])
+    b = b.cuda().double().permute(r["perm1"]).contiguous().reshape(r["I"], r["C"], r["L1"])
+    mid = torch.bmm(a, b).reshape(r["mid_shape"])
+    return mid.permute(r["out_perm"]).contiguous()

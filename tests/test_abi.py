@@ -1,0 +1,133 @@
+"""The C ABI: the core library loads and exports every function
+include/pto_einsum_hip.h declares; per-shape libraries export the reference's
+ctypes symbol set (builder.py:761-815); the ctypes struct mirrors match the C
+layout.  No compute calls (no GPU needed)."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+import torch
+
+from pto_einsum import EinsumBuilder, abi, runtime
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "pto_einsum_hip.h")
+PER_SHAPE = {"run_einsum", "run_einsum_setup", "run_einsum_exec", "run_einsum_teardown",
+             "run_transpose_inp0", "run_transpose_inp1", "run_transpose_out", "run_batched_matmul"}
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b((?:pe|run)_[a-z0-9_]+)\s*\(", text))
+
+
+def exported(path):
+    out = subprocess.run(["nm", "-D", "--defined-only", path], capture_output=True, text=True, check=True).stdout
+    return {line.split()[-1] for line in out.splitlines() if " T " in line}
+
+
+def test_core_exports_every_declared_function():
+    decl = declared_functions()
+    core = decl - PER_SHAPE
+    assert {"pe_product", "pe_permute", "pe_gemm", "pe_einsum_exec", "pe_einsum_setup"} <= core
+    missing = core - exported(runtime.core_library_path())
+    assert not missing, f"core library lacks {missing}"
+    lib = runtime.core()
+    for name in core:
+        getattr(lib, name)
+    assert b"gfx950" in lib.pe_version()
+
+
+@pytest.mark.parametrize("eq,s0,s1,expect", [
+    ("bji,bjk->bik", (2, 7, 10), (2, 7, 15), PER_SHAPE),
+    ("ts,ts->ts", (8, 16), (8, 16), {"run_einsum", "run_einsum_setup", "run_einsum_exec", "run_einsum_teardown"}),
+    ("bsd,d->bsd", (2, 8, 16), (16,), {"run_einsum", "run_einsum_setup", "run_einsum_exec", "run_einsum_teardown"}),
+])
+def test_per_shape_library_symbols(eq, s0, s1, expect, tmp_path, monkeypatch):
+    monkeypatch.setenv("EINSUM_BUILD_DIR", str(tmp_path))
+    b = EinsumBuilder(eq, [s0, s1], torch.float16)
+    b.build()
+    syms = exported(b.so_filename)
+    assert expect <= syms
+    assert not (PER_SHAPE - expect) & syms
+    assert declared_functions() >= PER_SHAPE
+    assert os.path.exists(b.cpp_filename) and b.target_dir.startswith(str(tmp_path))
+    b.cleanup()
+    assert not os.path.exists(b.target_dir)
+
+
+def test_cache_reuses_library(tmp_path, monkeypatch):
+    monkeypatch.setenv("EINSUM_BUILD_DIR", str(tmp_path))
+    b1 = EinsumBuilder("ij,jk->ik", [(4, 5), (5, 6)], torch.float32)
+    b1.build()
+    mtime = os.path.getmtime(b1.so_filename)
+    b2 = EinsumBuilder("ij,jk->ik", [(4, 5), (5, 6)], torch.float32)
+    b2.build()
+    assert b2.so_filename == b1.so_filename and os.path.getmtime(b2.so_filename) == mtime
+    monkeypatch.setenv("EINSUM_EXTRA_DEFINES", "-DPE_TAG=1")
+    b3 = EinsumBuilder("ij,jk->ik", [(4, 5), (5, 6)], torch.float32)
+    b3.build()
+    assert b3.so_filename != b1.so_filename
+
+
+def test_compile_failure_raises(tmp_path, monkeypatch):
+    monkeypatch.setenv("EINSUM_BUILD_DIR", str(tmp_path))
+    monkeypatch.setenv("EINSUM_EXTRA_DEFINES", "-DPE_BROKEN=1 -include /nonexistent/header.h")
+    b = EinsumBuilder("ij,jk->ik", [(4, 5), (5, 6)], torch.float32)
+    with pytest.raises(RuntimeError, match="Compilation failed"):
+        b.build()
+
+
+STRUCT_PROBE = r"""
+#include <cstddef>
+#include <cstdio>
+#include "pto_einsum_hip.h"
+#define OFF(T, f) printf(#T "." #f " %zu\n", offsetof(T, f))
+int main() {
+  printf("pe_product_desc %zu\npe_permute_desc %zu\npe_gemm_desc %zu\npe_einsum_plan %zu\n",
+         sizeof(pe_product_desc), sizeof(pe_permute_desc), sizeof(pe_gemm_desc), sizeof(pe_einsum_plan));
+  OFF(pe_product_desc, b_numel); OFF(pe_permute_desc, src_numel); OFF(pe_gemm_desc, M);
+  OFF(pe_gemm_desc, c_numel); OFF(pe_einsum_plan, gemm); OFF(pe_einsum_plan, ws_bytes);
+  return 0;
+}
+"""
+
+
+def test_ctypes_struct_layout_matches_c(tmp_path):
+    src = tmp_path / "probe.cpp"
+    src.write_text(STRUCT_PROBE)
+    exe = tmp_path / "probe"
+    subprocess.run(["g++", "-std=c++17", "-I", os.path.dirname(HEADER), str(src), "-o", str(exe)], check=True)
+    vals = dict(line.rsplit(" ", 1) for line in subprocess.run([str(exe)], capture_output=True, text=True,
+                                                                  check=True).stdout.splitlines())
+    assert int(vals["pe_product_desc"]) == ctypes.sizeof(abi.ProductDesc)
+    assert int(vals["pe_permute_desc"]) == ctypes.sizeof(abi.PermuteDesc)
+    assert int(vals["pe_gemm_desc"]) == ctypes.sizeof(abi.GemmDesc)
+    assert int(vals["pe_einsum_plan"]) == ctypes.sizeof(abi.EinsumPlan)
+    assert int(vals["pe_product_desc.b_numel"]) == abi.ProductDesc.b_numel.offset
+    assert int(vals["pe_permute_desc.src_numel"]) == abi.PermuteDesc.src_numel.offset
+    assert int(vals["pe_gemm_desc.M"]) == abi.GemmDesc.M.offset
+    assert int(vals["pe_gemm_desc.c_numel"]) == abi.GemmDesc.c_numel.offset
+    assert int(vals["pe_einsum_plan.gemm"]) == abi.EinsumPlan.gemm.offset
+    assert int(vals["pe_einsum_plan.ws_bytes"]) == abi.EinsumPlan.ws_bytes.offset
+
+
+def test_descriptor_validation_rejects_out_of_bounds():
+    """Host-side checks refuse descriptors that would address past an
+    operand, before anything is launched (null pointers, no GPU touched)."""
+    lib = abi.bind()
+    d = abi.GemmDesc()
+    d.dtype, d.M, d.N, d.K = 0, 4, 4, 4
+    d.a_ms, d.a_ks, d.b_ks, d.b_ns, d.c_ms, d.c_ns = 4, 1, 4, 1, 4, 1
+    d.a_numel, d.b_numel, d.c_numel = 15, 16, 16   # A is one element short
+    assert lib.pe_gemm(ctypes.byref(d), None, None, None, None, 0, None) == -2
+    assert b"operand 0" in lib.pe_last_error()
+    p = abi.PermuteDesc()
+    p.elem_bytes, p.ndims, p.src_numel = 4, 2, 11
+    p.shape[0], p.shape[1], p.src_stride[0], p.src_stride[1] = 3, 4, 1, 3
+    assert lib.pe_permute(ctypes.byref(p), None, None, None) == -2
+    q = abi.ProductDesc()
+    q.dtype, q.ndims, q.a_numel, q.b_numel = 3, 0, 1, 1
+    assert lib.pe_product(ctypes.byref(q), None, None, None, None) == -3
