@@ -11,9 +11,18 @@ route (cpu_einsum.h compiled by oracle/ref_build.py; the C restatement in
 oracle/ when that build is absent) on one of the 16 batches.
 
 ``per_config`` adds every other BASELINE equation at full size with its own
-binding roof (HBM bytes or MFMA flops), measured the same way.
+binding roof (HBM bytes or MFMA flops).  Those kernels run for tens of
+microseconds, less than one Python-level call costs, so each is captured once
+in a HIP graph and the graph is replayed between two events: the figure is the
+GPU time of the einsum's launches.
+
+``roofline.traffic`` (HBM bytes per launch of the headline GEMM) is read from
+profiles/gemm_f32_config2_traffic.json, written from two rocprofv3 --pmc runs
+(FETCH_SIZE, WRITE_SIZE) of this script, scaled by the same counters on
+``--copy-probe`` (a plain copy of known size).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-configs]
+       python bench.py --copy-probe     # counter calibration: one 1 GiB copy
 """
 import argparse
 import json
@@ -40,6 +49,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-configs", action="store_true", help="headline workload only")
     ap.add_argument("--cpu-sample-batches", type=int, default=1)
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="run a plain 1 GiB device copy (counter calibration) and exit")
     return ap.parse_args()
 
 
@@ -64,6 +75,68 @@ def time_runner(run, a, b, steps, warmup):
     torch.cuda.synchronize()
     per = [s.elapsed_time(e) for s, e in ev]
     return per, t0.elapsed_time(t1)
+
+
+def time_graph(run, a, b, steps, warmup, out_bytes):
+    """GPU time (ms) of one einsum: `reps` calls are captured in one HIP graph
+    (graph launch overhead paid once per replay), the graph is replayed
+    `steps` times between events, and the median per-call time is returned."""
+    import torch
+
+    reps = int(max(1, min(20, (8 << 30) // max(1, out_bytes))))
+    for _ in range(max(2, warmup)):
+        run(a, b)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(reps):
+            run(a, b)
+    for _ in range(2):
+        g.replay()
+    torch.cuda.synchronize()
+    per = []
+    for _ in range(max(3, steps // 4)):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        per.append(e0.elapsed_time(e1) / reps)
+    del g
+    torch.cuda.empty_cache()
+    return statistics.median(per)
+
+
+def copy_probe():
+    """A 1 GiB float32 copy through the core library's permutation launcher
+    (identity permutation = plain copy): reads and writes exactly 1 GiB."""
+    import ctypes
+
+    import torch
+
+    from pto_einsum import abi, launch
+
+    n = 1 << 28
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    lib = abi.bind()
+    d = abi.permute_desc(launch.PermuteDesc(4, [n], [1], n))
+    for _ in range(5):
+        rc = lib.pe_permute(ctypes.byref(d), ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(dst.data_ptr()),
+                            ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        assert rc == 0
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes_each_way": n * 4, "launches": 5}))
+
+
+def traffic_from_profile():
+    path = os.path.join(ROOT, "profiles", "gemm_f32_config2_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
 
 
 def config_list():
@@ -171,6 +244,9 @@ def main():
     from pto_einsum import EinsumBuilder
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.copy_probe:
+        copy_probe()
+        return
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
 
@@ -188,7 +264,7 @@ def main():
     ms_per_step = total_ms / args.steps
     kernel_ms = statistics.mean(per)
     roof, _, _ = roofline(flops, nbytes, kernel_ms, "f32")
-    roof["traffic"] = None
+    roof["traffic"] = traffic_from_profile()
     value = flops / (ms_per_step * 1e-3) / 1e12
     log(f"bench: config 2 {ms_per_step * 1e3:.1f} us/step, kernel {kernel_ms * 1e3:.1f} us, {value:.2f} TFLOP/s")
 
@@ -199,10 +275,9 @@ def main():
             x, y = gen(gg)
             x, y = x.to(dev), y.to(dev)
             r = EinsumBuilder(ceq, [tuple(x.shape), tuple(y.shape)], x.dtype).build()
-            steps = max(5, args.steps // 2)
-            p, _ = time_runner(r, x, y, steps, max(3, args.warmup // 2))
             f, nb = work(ceq, x, y)
-            km = statistics.median(p)
+            km = time_graph(r, x, y, max(10, args.steps), max(3, args.warmup // 2),
+                            r(x, y).numel() * 4)
             rf, tf, gb = roofline(f, nb, km, dt)
             per_config.append(dict(config=name, equation=ceq, dtype=dt, us=round(km * 1e3, 2),
                                    tflops=round(tf, 3), gbs=round(gb, 1), roof=rf["bound"],

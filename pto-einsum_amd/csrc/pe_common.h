@@ -80,6 +80,22 @@ struct F16 {
     __device__ __forceinline__ static float to_f32(_Float16 x) { return (float)x; }
 };
 
+// Outputs at least this large stream past the caches with non-temporal
+// stores; smaller ones (which fit the 256 MB Infinity Cache) use ordinary
+// stores, which measured faster there.
+#ifndef PE_NT_MIN_BYTES
+#define PE_NT_MIN_BYTES (128ll << 20)
+#endif
+
+__device__ __forceinline__ void store_f(float* p, float v, bool nt) {
+    if (nt) __builtin_nontemporal_store(v, p);
+    else *p = v;
+}
+__device__ __forceinline__ void store_f(f32x4* p, f32x4 v, bool nt) {
+    if (nt) __builtin_nontemporal_store(v, p);
+    else *p = v;
+}
+
 __device__ __forceinline__ void store_nt(float* p, float v) {
     __builtin_nontemporal_store(v, p);
 }

@@ -53,6 +53,8 @@ struct GemmArgs {
     uint32_t tiles_per_batch; // tiles_m * tiles_n
     uint32_t nbatch_total;
     uint32_t total_blocks;    // tiles_per_batch * nbatch_total * nsplit
+    uint32_t grid;            // launched blocks (persistent when < total_blocks)
+    int32_t store_nt;         // non-temporal stores for the output
     int64_t a_ms, a_ks, b_ks, b_ns, c_ms, c_ns;
     int32_t nbatch;
     FastDiv batch_div[PE_MAX_DIMS];
@@ -67,13 +69,20 @@ struct ReduceArgs {
     FastDiv n_div, m_div;     // flat -> (batch, m, n)
     int64_t c_ms, c_ns;
     int32_t nbatch;
+    int32_t store_nt;
     FastDiv batch_div[PE_MAX_DIMS];
     int64_t c_bs[PE_MAX_DIMS];
 };
 
 // Host-side launch entry for one (dtype, tile) family; defined per family
 // in pe_gemm_f32.hip / pe_gemm_f16.hip.
-hipError_t launch_gemm_f32(int bm, int alayout, int blayout, const GemmArgs& g, hipStream_t s);
-hipError_t launch_gemm_f16(int bm, int alayout, int blayout, const GemmArgs& g, hipStream_t s);
+// Slab depth (k per LDS stage) of each family, for the split-K granularity.
+int gemm_bk(int dtype);
+// (bm, bn) is one of 64x64, 128x128, 256x128, 128x256.  gemm_occupancy_*
+// returns resident blocks per CU of that tile (runtime occupancy query).
+int gemm_occupancy_f32(int bm, int bn);
+int gemm_occupancy_f16(int bm, int bn);
+hipError_t launch_gemm_f32(int bm, int bn, int alayout, int blayout, const GemmArgs& g, hipStream_t s);
+hipError_t launch_gemm_f16(int bm, int bn, int alayout, int blayout, const GemmArgs& g, hipStream_t s);
 
 }  // namespace pe

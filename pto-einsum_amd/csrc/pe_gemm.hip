@@ -5,6 +5,20 @@
 
 #include <algorithm>
 
+// Resident blocks per CU when the tile loop is persistent; 0 launches one
+// block per tile.
+#ifndef PE_GEMM_PERSIST
+#define PE_GEMM_PERSIST 0
+#endif
+// 256x128 / 128x256 tiles (wave tile 128x64) for grids that still fill the
+// GPU, with their own persistent block count.
+#ifndef PE_GEMM_BIG
+#define PE_GEMM_BIG 1
+#endif
+#ifndef PE_GEMM_BIG_PERSIST
+#define PE_GEMM_BIG_PERSIST 0
+#endif
+
 namespace pe {
 
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(ReduceArgs r) {
@@ -22,14 +36,15 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(ReduceArgs r) {
             off += int64_t(rr) * r.c_bs[d];
             batch = q;
         }
-        store_nt(r.c + off, acc);
+        store_f(r.c + off, acc, r.store_nt != 0);
     }
 }
 
 namespace {
 
 struct GemmChoice {
-    int bm;        // square tile edge, 64 or 128
+    int bm, bn;    // tile: 64x64, 128x128, 256x128 or 128x256
+    int persist;   // blocks per CU of a persistent grid (0: one block per tile)
     int nsplit;    // K splits (1 = direct store)
     int k_per_split;
     int64_t nbatch_total;
@@ -45,15 +60,37 @@ int64_t batch_total(const pe_gemm_desc& d) {
 GemmChoice choose(const pe_gemm_desc& d) {
     GemmChoice c{};
     c.nbatch_total = batch_total(d);
-    const int bk = d.dtype == PE_F32 ? 16 : 32;
+    const int bk = gemm_bk(d.dtype);
     const int64_t cus = cu_count();
+    c.persist = PE_GEMM_PERSIST;
     if (d.tile == 64 || d.tile == 128) {
-        c.bm = d.tile;
+        c.bm = c.bn = d.tile;
     } else {
         c.bm = (d.M > 64 && d.N > 64) ? 128 : 64;
         if (c.bm == 128 && c.nbatch_total * ceil_div(d.M, 128) * ceil_div(d.N, 128) < cus) c.bm = 64;
+        c.bn = c.bm;
+        if (PE_GEMM_BIG && c.bm == 128 && d.dtype == PE_F32) {
+            // 256x128 tiles halve the fragment reads per MFMA but hold only
+            // two waves per SIMD.  Pick the tiling whose tiles fill the
+            // resident slots most evenly; the larger tile gets the ~12 % edge
+            // measured on large square problems.
+            auto util = [&](int bm, int bn) {
+                const int64_t t = c.nbatch_total * ceil_div(d.M, bm) * ceil_div(d.N, bn);
+                const int64_t slots = cus * gemm_occupancy_f32(bm, bn);
+                const int64_t rounds = ceil_div(t, slots);
+                return double(t) / double(rounds * slots);
+            };
+            const bool tall = d.M >= d.N;
+            const int bbm = tall ? 256 : 128, bbn = tall ? 128 : 256;
+            const int64_t bt = c.nbatch_total * ceil_div(d.M, bbm) * ceil_div(d.N, bbn);
+            if (bt >= cus && util(bbm, bbn) * 1.12 > util(128, 128)) {
+                c.bm = bbm;
+                c.bn = bbn;
+                c.persist = PE_GEMM_BIG_PERSIST;
+            }
+        }
     }
-    const int64_t tiles = c.nbatch_total * ceil_div(d.M, c.bm) * ceil_div(d.N, c.bm);
+    const int64_t tiles = c.nbatch_total * ceil_div(d.M, c.bm) * ceil_div(d.N, c.bn);
     int64_t split = 1;
     if (d.split_k > 0) {
         split = d.split_k;
@@ -179,10 +216,16 @@ extern "C" int pe_gemm(const pe_gemm_desc* d, const void* a, const void* b, floa
     g.nsplit = ch.nsplit;
     g.k_per_split = ch.k_per_split;
     g.tiles_m = int32_t(ceil_div(d->M, ch.bm));
-    g.tiles_n = int32_t(ceil_div(d->N, ch.bm));
+    g.tiles_n = int32_t(ceil_div(d->N, ch.bn));
     g.tiles_per_batch = uint32_t(g.tiles_m) * uint32_t(g.tiles_n);
     g.nbatch_total = uint32_t(nb);
     g.total_blocks = g.tiles_per_batch * g.nbatch_total * uint32_t(ch.nsplit);
+    g.grid = g.total_blocks;
+    g.store_nt = (ch.nsplit > 1 ? ch.ws_bytes : nb * d->M * d->N * 4) >= PE_NT_MIN_BYTES;
+    if (ch.persist > 0) {
+        const uint32_t cap = uint32_t(cu_count()) * uint32_t(ch.persist);
+        if (g.grid > cap) g.grid = cap;
+    }
     g.a_ms = d->a_ms; g.a_ks = d->a_ks; g.b_ks = d->b_ks; g.b_ns = d->b_ns;
     g.c_ms = d->c_ms; g.c_ns = d->c_ns;
     g.nbatch = d->nbatch;
@@ -192,12 +235,13 @@ extern "C" int pe_gemm(const pe_gemm_desc* d, const void* a, const void* b, floa
         g.b_bs[i] = d->b_bstride[i];
         g.c_bs[i] = d->c_bstride[i];
     }
-    hipError_t e = d->dtype == PE_F32 ? launch_gemm_f32(ch.bm, al, bl, g, s)
-                                      : launch_gemm_f16(ch.bm, al, bl, g, s);
+    hipError_t e = d->dtype == PE_F32 ? launch_gemm_f32(ch.bm, ch.bn, al, bl, g, s)
+                                      : launch_gemm_f16(ch.bm, ch.bn, al, bl, g, s);
     PE_CHECK_HIP(e);
     if (ch.nsplit > 1) {
         r.nsplit = ch.nsplit;
         r.partial = static_cast<const float*>(ws);
+        r.store_nt = nb * d->M * d->N * 4 >= PE_NT_MIN_BYTES;
         hipLaunchKernelGGL(splitk_reduce_kernel, dim3(reduce_grid()), dim3(256), 0, s, r);
         PE_CHECK_HIP(hipGetLastError());
     }

@@ -1,35 +1,68 @@
 // float32 instantiations of the batched MFMA GEMM (v_mfma_f32_32x32x2_f32).
 #include "pe_gemm_kernel.h"
 
+// Slab depth and LDS layout for float32 (see GemmGeom).
+#ifndef PE_GEMM_F32_BK
+#define PE_GEMM_F32_BK 16
+#endif
+#ifndef PE_GEMM_F32_KC
+#define PE_GEMM_F32_KC 0
+#endif
+#ifndef PE_GEMM_F32_NBUF
+#define PE_GEMM_F32_NBUF 1
+#endif
+
 namespace pe {
 
-template <int BM, int AL, int BL>
+template <int BM, int BN, int AL, int BL>
 static hipError_t go(const GemmArgs& g, hipStream_t s) {
-    hipLaunchKernelGGL((gemm_kernel<F32, BM, BM, AL, BL>), dim3(g.total_blocks),
+    hipLaunchKernelGGL((gemm_kernel<F32, BM, BN, PE_GEMM_F32_BK, bool(PE_GEMM_F32_KC), PE_GEMM_F32_NBUF, AL, BL>), dim3(g.grid),
                        dim3(kGemmThreads), 0, s, g);
     return hipGetLastError();
 }
 
-template <int BM, int AL>
+template <int BM, int BN, int AL>
 static hipError_t go_b(int bl, const GemmArgs& g, hipStream_t s) {
     switch (bl) {
-        case L_MN: return go<BM, AL, L_MN>(g, s);
-        case L_K: return go<BM, AL, L_K>(g, s);
-        default: return go<BM, AL, L_GENERIC>(g, s);
+        case L_MN: return go<BM, BN, AL, L_MN>(g, s);
+        case L_K: return go<BM, BN, AL, L_K>(g, s);
+        default: return go<BM, BN, AL, L_GENERIC>(g, s);
     }
 }
 
-template <int BM>
+template <int BM, int BN>
 static hipError_t go_a(int al, int bl, const GemmArgs& g, hipStream_t s) {
     switch (al) {
-        case L_MN: return go_b<BM, L_MN>(bl, g, s);
-        case L_K: return go_b<BM, L_K>(bl, g, s);
-        default: return go_b<BM, L_GENERIC>(bl, g, s);
+        case L_MN: return go_b<BM, BN, L_MN>(bl, g, s);
+        case L_K: return go_b<BM, BN, L_K>(bl, g, s);
+        default: return go_b<BM, BN, L_GENERIC>(bl, g, s);
     }
 }
 
-hipError_t launch_gemm_f32(int bm, int al, int bl, const GemmArgs& g, hipStream_t s) {
-    return bm == 128 ? go_a<128>(al, bl, g, s) : go_a<64>(al, bl, g, s);
+int gemm_bk_f16();
+int gemm_bk(int dtype) { return dtype == PE_F32 ? PE_GEMM_F32_BK : gemm_bk_f16(); }
+
+template <int BM, int BN>
+static int occ() {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &n, reinterpret_cast<const void*>(&gemm_kernel<F32, BM, BN, PE_GEMM_F32_BK, bool(PE_GEMM_F32_KC), PE_GEMM_F32_NBUF, L_MN, L_MN>),
+            kGemmThreads, 0) != hipSuccess || n < 1)
+        n = 1;
+    return n;
+}
+
+int gemm_occupancy_f32(int bm, int bn) {
+    static const int o[4] = {occ<64, 64>(), occ<128, 128>(), occ<256, 128>(), occ<128, 256>()};
+    if (bm == 256) return o[2];
+    if (bn == 256) return o[3];
+    return bm == 128 ? o[1] : o[0];
+}
+
+hipError_t launch_gemm_f32(int bm, int bn, int al, int bl, const GemmArgs& g, hipStream_t s) {
+    if (bm == 256) return go_a<256, 128>(al, bl, g, s);
+    if (bn == 256) return go_a<128, 256>(al, bl, g, s);
+    return bm == 128 ? go_a<128, 128>(al, bl, g, s) : go_a<64, 64>(al, bl, g, s);
 }
 
 }  // namespace pe

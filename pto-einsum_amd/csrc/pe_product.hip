@@ -24,6 +24,23 @@
 #include <algorithm>
 #include <vector>
 
+// Blocks per CU of the grid-stride stream and vectors per thread per
+// iteration.  Measured on MI355X: a flat contiguous stream runs fastest with
+// few long-lived waves (a compact moving window in HBM); streams that decode
+// outer axes per vector need many more waves to hide that arithmetic.
+#ifndef PE_PRODUCT_GRID_PER_CU_FLAT
+#define PE_PRODUCT_GRID_PER_CU_FLAT 2
+#endif
+#ifndef PE_PRODUCT_GRID_PER_CU
+#define PE_PRODUCT_GRID_PER_CU 64
+#endif
+#ifndef PE_PRODUCT_UNROLL
+#define PE_PRODUCT_UNROLL 1
+#endif
+#ifndef PE_PRODUCT_VEC
+#define PE_PRODUCT_VEC 4
+#endif
+
 namespace pe {
 namespace {
 
@@ -42,6 +59,7 @@ struct ProductArgs {
     int64_t a_outer[kMaxOuter];
     int64_t b_outer[kMaxOuter];
     int64_t a_inner, b_inner;
+    int32_t nt;             // non-temporal output stores
 };
 
 template <typename E, int VEC>
@@ -60,6 +78,14 @@ struct VecLoad<F16, 8> {
         f16x8 x = *reinterpret_cast<const f16x8*>(p);
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[i] = (float)x[i];
+    }
+};
+template <>
+struct VecLoad<F16, 4> {
+    __device__ __forceinline__ static void load(const _Float16* p, float (&v)[4]) {
+        f16x4 x = *reinterpret_cast<const f16x4*>(p);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = (float)x[i];
     }
 };
 template <typename E>
@@ -87,18 +113,18 @@ __device__ __forceinline__ void load_b(const typename E::T* b, int64_t off, int6
 }
 
 template <int VEC>
-__device__ __forceinline__ void store_out(float* out, const float (&r)[VEC]) {
+__device__ __forceinline__ void store_out(float* out, const float (&r)[VEC], bool nt) {
     if constexpr (VEC == 4) {
         f32x4 v = {r[0], r[1], r[2], r[3]};
-        store_nt(reinterpret_cast<f32x4*>(out), v);
+        store_f(reinterpret_cast<f32x4*>(out), v, nt);
     } else if constexpr (VEC == 8) {
         f32x4 v0 = {r[0], r[1], r[2], r[3]};
         f32x4 v1 = {r[4], r[5], r[6], r[7]};
-        store_nt(reinterpret_cast<f32x4*>(out), v0);
-        store_nt(reinterpret_cast<f32x4*>(out) + 1, v1);
+        store_f(reinterpret_cast<f32x4*>(out), v0, nt);
+        store_f(reinterpret_cast<f32x4*>(out) + 1, v1, nt);
     } else {
 #pragma unroll
-        for (int i = 0; i < VEC; ++i) store_nt(out + i, r[i]);
+        for (int i = 0; i < VEC; ++i) store_f(out + i, r[i], nt);
     }
 }
 
@@ -155,7 +181,7 @@ __global__ __launch_bounds__(kThreads) void product_kernel(ProductArgs p) {
                 float prod = ra[u][i] * rb[u][i];
                 r[i] = ADD_ZERO ? 0.0f + prod : prod;
             }
-            store_out<VEC>(out + int64_t(v + u * stride) * VEC, r);
+            store_out<VEC>(out + int64_t(v + u * stride) * VEC, r, p.nt != 0);
         }
     }
 }
@@ -199,16 +225,17 @@ void merge_axes(const pe_product_desc& d, std::vector<int64_t>& shape,
     }
 }
 
-int grid_for(int64_t work_items, int per_block) {
+int grid_for(int64_t work_items, int per_block, int per_cu = PE_PRODUCT_GRID_PER_CU) {
     int64_t blocks = ceil_div(std::max<int64_t>(work_items, 1), per_block);
-    int64_t cap = int64_t(cu_count()) * 16;  // enough resident waves to cover HBM latency
+    int64_t cap = int64_t(cu_count()) * per_cu;
     return int(std::max<int64_t>(1, std::min(blocks, cap)));
 }
 
 template <typename E, int VEC, int B_MODE, bool ADD_ZERO, bool HAS_OUTER>
 hipError_t launch_vec(const ProductArgs& args, hipStream_t s) {
-    constexpr int U = (VEC >= 4) ? 2 : 4;
-    int grid = grid_for(ceil_div(args.nvec, U), kThreads);
+    constexpr int U = (VEC >= 4) ? PE_PRODUCT_UNROLL : 4;
+    int grid = grid_for(ceil_div(args.nvec, U), kThreads,
+                        HAS_OUTER ? PE_PRODUCT_GRID_PER_CU : PE_PRODUCT_GRID_PER_CU_FLAT);
     hipLaunchKernelGGL((product_kernel<E, VEC, B_MODE, ADD_ZERO, HAS_OUTER, U>), dim3(grid),
                        dim3(kThreads), 0, s, args);
     return hipGetLastError();
@@ -251,6 +278,7 @@ int run(const pe_product_desc& d, const void* in0, const void* in1, float* out,
 
     ProductArgs args{};
     args.a = in0; args.b = in1; args.out = out;
+    args.nt = n * 4 >= PE_NT_MIN_BYTES;
     const int nd = int(shape.size());
     const int64_t inner = nd ? shape[nd - 1] : 1;
     args.inner = uint32_t(inner);
@@ -263,13 +291,16 @@ int run(const pe_product_desc& d, const void* in0, const void* in1, float* out,
         args.b_outer[k] = sb[k];
     }
 
-    // Vector path: 16-byte loads of in0 along the innermost axis.  Needs a
-    // unit inner stride, an inner extent and outer strides that are whole
-    // vectors, and vector-aligned base pointers.
-    constexpr int VEC = 16 / E::kBytes;
+    // Vector path: VEC elements per lane along the innermost axis.  Four
+    // elements give one 16-byte float32 store per lane, so each wave-wide
+    // store covers 1 KB contiguously (float16 inputs load 8 bytes per lane).
+    // Needs a unit inner stride, an inner extent and outer strides that are
+    // whole vectors, and vector-aligned base pointers.
+    constexpr int VEC = PE_PRODUCT_VEC;
+    constexpr size_t VB = size_t(VEC) * E::kBytes;
     bool vec_ok = nd > 0 && args.a_inner == 1 && (args.b_inner == 0 || args.b_inner == 1) &&
-                  inner % VEC == 0 && aligned(in0, 16) && aligned(out, 16) &&
-                  (args.b_inner == 0 || aligned(in1, 16));
+                  inner % VEC == 0 && aligned(in0, VB) && aligned(out, 16) &&
+                  (args.b_inner == 0 || aligned(in1, VB));
     for (int k = 0; k < args.nouter && vec_ok; ++k)
         vec_ok = (sa[k] % VEC == 0) && (args.b_inner == 0 || sb[k] % VEC == 0);
     const bool has_outer = args.nouter > 0;
