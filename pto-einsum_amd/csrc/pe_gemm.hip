@@ -95,8 +95,8 @@ GemmChoice choose(const pe_gemm_desc& d) {
     if (d.split_k > 0) {
         split = d.split_k;
     } else if (tiles < cus && c.nbatch_total * d.M * d.N < (int64_t(1) << 32)) {
-        // Fill about two blocks per CU, keeping at least four K slabs per split.
-        split = std::min<int64_t>(ceil_div(2 * cus, tiles), std::max<int64_t>(1, d.K / (4 * bk)));
+        // Fill about four blocks per CU, keeping at least four K slabs per split.
+        split = std::min<int64_t>(ceil_div(4 * cus, tiles), std::max<int64_t>(1, d.K / (4 * bk)));
         split = std::max<int64_t>(1, std::min<int64_t>(split, 32));
     }
     int64_t kps = ceil_div(ceil_div(d.K, split), bk) * bk;

@@ -27,6 +27,16 @@ namespace {
 
 constexpr int kThreads = 256;
 
+// Gather stream shape (measured on MI355X with a plain copy: many resident
+// waves, two 16-byte vectors in flight per lane, non-temporal stores for
+// outputs larger than the Infinity Cache).
+#ifndef PE_GATHER_GRID_PER_CU
+#define PE_GATHER_GRID_PER_CU 64
+#endif
+#ifndef PE_GATHER_UNROLL
+#define PE_GATHER_UNROLL 2
+#endif
+
 struct GatherArgs {
     const void* src;
     void* dst;
@@ -36,6 +46,7 @@ struct GatherArgs {
     FastDiv outer_div[PE_MAX_DIMS];
     int64_t outer_stride[PE_MAX_DIMS];
     int64_t inner_stride;    // source stride of the innermost destination axis
+    int32_t nt;              // non-temporal stores
 };
 
 template <typename W, int VEC>
@@ -43,32 +54,51 @@ struct Chunk {
     W v[VEC];
 };
 
-// Streamed gather: VEC elements of type W per vector (16 bytes when VEC > 1).
-template <typename W, int VEC, bool HAS_OUTER>
+template <typename V>
+__device__ __forceinline__ void put(V* p, const V& v, bool nt) {
+    if (nt) __builtin_nontemporal_store(v, p);
+    else *p = v;
+}
+
+// Streamed gather: VEC elements of type W per vector (16 bytes when VEC > 1),
+// U vectors per lane in flight.
+template <typename W, int VEC, bool HAS_OUTER, int U>
 __global__ __launch_bounds__(kThreads) void gather_kernel(GatherArgs p) {
     const W* __restrict__ src = static_cast<const W*>(p.src);
     W* __restrict__ dst = static_cast<W*>(p.dst);
     const uint32_t stride = gridDim.x * kThreads;
-    for (uint32_t v = blockIdx.x * kThreads + threadIdx.x; v < p.nvec; v += stride) {
-        int64_t off;
-        if constexpr (HAS_OUTER) {
-            uint32_t row, colv;
-            p.inner_vecs.divmod(v, row, colv);
-            off = int64_t(colv) * VEC * p.inner_stride;
-            for (int d = p.nouter - 1; d >= 0; --d) {
-                uint32_t q, r;
-                p.outer_div[d].divmod(row, q, r);
-                off += int64_t(r) * p.outer_stride[d];
-                row = q;
+    for (uint32_t v0 = blockIdx.x * kThreads + threadIdx.x; v0 < p.nvec; v0 += stride * U) {
+        int64_t off[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t v = v0 + u * stride;
+            if constexpr (HAS_OUTER) {
+                uint32_t row, colv;
+                p.inner_vecs.divmod(v, row, colv);
+                off[u] = int64_t(colv) * VEC * p.inner_stride;
+                for (int d = p.nouter - 1; d >= 0; --d) {
+                    uint32_t q, r;
+                    p.outer_div[d].divmod(row, q, r);
+                    off[u] += int64_t(r) * p.outer_stride[d];
+                    row = q;
+                }
+            } else {
+                off[u] = int64_t(v) * VEC * p.inner_stride;
             }
-        } else {
-            off = int64_t(v) * VEC * p.inner_stride;
         }
         if constexpr (VEC > 1) {
-            using V = Chunk<W, VEC>;
-            *reinterpret_cast<V*>(dst + int64_t(v) * VEC) = *reinterpret_cast<const V*>(src + off);
+            u32x4 x[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                if (v0 + u * stride < p.nvec) x[u] = *reinterpret_cast<const u32x4*>(src + off[u]);
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                if (v0 + u * stride < p.nvec)
+                    put(reinterpret_cast<u32x4*>(dst + int64_t(v0 + u * stride) * VEC), x[u], p.nt != 0);
         } else {
-            dst[v] = src[off];
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                if (v0 + u * stride < p.nvec) dst[v0 + u * stride] = src[off[u]];
         }
     }
 }
@@ -86,27 +116,44 @@ struct TileArgs {
     int64_t batch_src[PE_MAX_DIMS];
     int64_t batch_dst[PE_MAX_DIMS];
     uint32_t nbatch_total;
+    int32_t nt;
 };
 
 constexpr int kTile = 64;
 
-// One 64x64 tile per block: 256 threads read 64 rows (q) of 64 source-
-// contiguous elements (p), then write 64 rows (p) of 64 destination-
-// contiguous elements (q).
-template <typename W>
+#ifndef PE_TILE_GRID_PER_CU
+#define PE_TILE_GRID_PER_CU 32
+#endif
+
+// One 64x64 tile per block iteration.  With VLOAD the reads are 16-byte
+// vectors along p (source-contiguous), else one element per lane with the
+// lanes along p; with VSTORE the writes are 16-byte vectors along q
+// (destination-contiguous), else one element per lane with the lanes along q.
+// The LDS tile has one padding element per row, so the row-wise accesses of
+// one side and the column-wise accesses of the other both spread over all
+// banks.  Tiles are walked diagonally (the q-tile index is offset by the
+// p-tile index), so concurrently running blocks do not all write rows that
+// are a large power of two apart in the same column range.
+template <typename W, bool VLOAD, bool VSTORE>
 __global__ __launch_bounds__(kThreads) void tile_transpose_kernel(TileArgs p) {
-    __shared__ W tile[kTile][kTile + 1];
+    constexpr int VEC = 16 / sizeof(W);
+    constexpr int LVPR = VLOAD ? kTile / VEC : kTile;   // lanes per tile row, read side
+    constexpr int LW = VLOAD ? VEC : 1;                  // elements per lane access, read
+    constexpr int SVPR = VSTORE ? kTile / VEC : kTile;  // lanes per tile row, write side
+    constexpr int SW = VSTORE ? VEC : 1;
+    __shared__ W tile[kTile][kTile + 1];  // tile[q][p]
     const W* __restrict__ src = static_cast<const W*>(p.src);
     W* __restrict__ dst = static_cast<W*>(p.dst);
     const uint32_t tiles_per_batch = p.tiles_p * p.tiles_q;
     const uint32_t total = tiles_per_batch * p.nbatch_total;
-    const int tx = threadIdx.x % kTile;
-    const int ty = threadIdx.x / kTile;  // 0..3
+    const int lc = threadIdx.x % LVPR, lr = threadIdx.x / LVPR;
+    const int sc = threadIdx.x % SVPR, sr = threadIdx.x / SVPR;
     for (uint32_t t = blockIdx.x; t < total; t += gridDim.x) {
         uint32_t bidx = t / tiles_per_batch;
-        uint32_t rem = t - bidx * tiles_per_batch;
-        uint32_t tq = rem / p.tiles_p;
-        uint32_t tp = rem - tq * p.tiles_p;
+        const uint32_t rem = t - bidx * tiles_per_batch;
+        const uint32_t tp = rem % p.tiles_p;
+        uint32_t tq = rem / p.tiles_p + tp;
+        tq = tq % p.tiles_q;
         int64_t sbase = 0, dbase = 0;
         for (int d = p.nbatch - 1; d >= 0; --d) {
             uint32_t q, r;
@@ -116,18 +163,40 @@ __global__ __launch_bounds__(kThreads) void tile_transpose_kernel(TileArgs p) {
             bidx = q;
         }
         const int64_t p0 = int64_t(tp) * kTile, q0 = int64_t(tq) * kTile;
-        const int64_t pi = p0 + tx;
+        // Read: tile rows are q, each lane covers LW consecutive p.
 #pragma unroll
-        for (int r = 0; r < kTile / 4; ++r) {
-            int64_t qi = q0 + ty + 4 * r;
-            if (pi < p.P && qi < p.Q) tile[ty + 4 * r][tx] = src[sbase + qi * p.src_q_stride + pi];
+        for (int r = lr; r < kTile; r += kThreads / LVPR) {
+            const int64_t gq = q0 + r, gp = p0 + lc * LW;
+            if (gq >= p.Q) continue;
+            const W* s = src + sbase + gq * p.src_q_stride + gp;
+            if (VLOAD && gp + LW <= p.P) {
+                Chunk<W, LW> x = *reinterpret_cast<const Chunk<W, LW>*>(s);
+#pragma unroll
+                for (int j = 0; j < LW; ++j) tile[r][lc * LW + j] = x.v[j];
+            } else {
+#pragma unroll
+                for (int j = 0; j < LW; ++j)
+                    if (gp + j < p.P) tile[r][lc * LW + j] = s[j];
+            }
         }
         __syncthreads();
-        const int64_t qo = q0 + tx;
+        // Write: destination rows are p, each lane covers SW consecutive q.
 #pragma unroll
-        for (int r = 0; r < kTile / 4; ++r) {
-            int64_t po = p0 + ty + 4 * r;
-            if (po < p.P && qo < p.Q) dst[dbase + po * p.dst_p_stride + qo] = tile[tx][ty + 4 * r];
+        for (int r = sr; r < kTile; r += kThreads / SVPR) {
+            const int64_t gp = p0 + r, gq = q0 + sc * SW;
+            if (gp >= p.P) continue;
+            W* d = dst + dbase + gp * p.dst_p_stride + gq;
+            if (VSTORE && gq + SW <= p.Q) {
+                Chunk<W, SW> x;
+#pragma unroll
+                for (int j = 0; j < SW; ++j) x.v[j] = tile[sc * SW + j][r];
+                if constexpr (VSTORE)
+                    put(reinterpret_cast<u32x4*>(d), *reinterpret_cast<const u32x4*>(&x), p.nt != 0);
+            } else {
+#pragma unroll
+                for (int j = 0; j < SW; ++j)
+                    if (gq + j < p.Q) d[j] = tile[sc * SW + j][r];
+            }
         }
         __syncthreads();
     }
@@ -149,8 +218,8 @@ __global__ __launch_bounds__(kThreads) void gather_wide_kernel(const W* __restri
     }
 }
 
-int grid_cap(int64_t blocks) {
-    int64_t cap = int64_t(cu_count()) * 16;
+int grid_cap(int64_t blocks, int per_cu = 16) {
+    int64_t cap = int64_t(cu_count()) * per_cu;
     return int(std::max<int64_t>(1, std::min(blocks, cap)));
 }
 
@@ -201,21 +270,24 @@ int run(const pe_permute_desc& d, const void* src, void* dst, hipStream_t s) {
             a.outer_stride[k] = sst[k];
         }
         constexpr int VEC = 16 / sizeof(W);
+        constexpr int U = PE_GATHER_UNROLL;
+        a.nt = n * int64_t(sizeof(W)) >= PE_NT_MIN_BYTES;
         bool vec = inner_kept && nd > 0 && inner % VEC == 0 && aligned(src, 16) && aligned(dst, 16);
         for (int k = 0; k < a.nouter && vec; ++k) vec = sst[k] % VEC == 0;
         const bool outer = a.nouter > 0;
+        const int per_cu = PE_GATHER_GRID_PER_CU;
         if (vec) {
             a.nvec = uint32_t(n / VEC);
             a.inner_vecs.init(uint32_t(inner / VEC));
-            int grid = grid_cap(ceil_div(a.nvec, kThreads));
-            if (outer) hipLaunchKernelGGL((gather_kernel<W, VEC, true>), dim3(grid), dim3(kThreads), 0, s, a);
-            else hipLaunchKernelGGL((gather_kernel<W, VEC, false>), dim3(grid), dim3(kThreads), 0, s, a);
+            int grid = grid_cap(ceil_div(ceil_div(a.nvec, U), kThreads), per_cu);
+            if (outer) hipLaunchKernelGGL((gather_kernel<W, VEC, true, U>), dim3(grid), dim3(kThreads), 0, s, a);
+            else hipLaunchKernelGGL((gather_kernel<W, VEC, false, U>), dim3(grid), dim3(kThreads), 0, s, a);
         } else {
             a.nvec = uint32_t(n);
             a.inner_vecs.init(uint32_t(inner));
-            int grid = grid_cap(ceil_div(a.nvec, kThreads));
-            if (outer) hipLaunchKernelGGL((gather_kernel<W, 1, true>), dim3(grid), dim3(kThreads), 0, s, a);
-            else hipLaunchKernelGGL((gather_kernel<W, 1, false>), dim3(grid), dim3(kThreads), 0, s, a);
+            int grid = grid_cap(ceil_div(ceil_div(a.nvec, 4), kThreads), per_cu);
+            if (outer) hipLaunchKernelGGL((gather_kernel<W, 1, true, 4>), dim3(grid), dim3(kThreads), 0, s, a);
+            else hipLaunchKernelGGL((gather_kernel<W, 1, false, 4>), dim3(grid), dim3(kThreads), 0, s, a);
         }
         PE_CHECK_HIP(hipGetLastError());
         return PE_OK;
@@ -242,8 +314,20 @@ int run(const pe_permute_desc& d, const void* src, void* dst, hipStream_t s) {
     }
     t.nbatch = nb;
     t.nbatch_total = uint32_t(nbt);
+    t.nt = n * int64_t(sizeof(W)) >= PE_NT_MIN_BYTES;
+    constexpr int VEC = 16 / sizeof(W);
+    bool vload = aligned(src, 16) && t.src_q_stride % VEC == 0;
+    bool vstore = aligned(dst, 16) && t.dst_p_stride % VEC == 0;
+    for (int k = 0; k < nb; ++k) {
+        vload = vload && t.batch_src[k] % VEC == 0;
+        vstore = vstore && t.batch_dst[k] % VEC == 0;
+    }
     int64_t tiles = int64_t(t.tiles_p) * t.tiles_q * nbt;
-    hipLaunchKernelGGL((tile_transpose_kernel<W>), dim3(grid_cap(tiles)), dim3(kThreads), 0, s, t);
+    const dim3 grid(grid_cap(tiles, PE_TILE_GRID_PER_CU));
+    if (vload && vstore) hipLaunchKernelGGL((tile_transpose_kernel<W, true, true>), grid, dim3(kThreads), 0, s, t);
+    else if (vload) hipLaunchKernelGGL((tile_transpose_kernel<W, true, false>), grid, dim3(kThreads), 0, s, t);
+    else if (vstore) hipLaunchKernelGGL((tile_transpose_kernel<W, false, true>), grid, dim3(kThreads), 0, s, t);
+    else hipLaunchKernelGGL((tile_transpose_kernel<W, false, false>), grid, dim3(kThreads), 0, s, t);
     PE_CHECK_HIP(hipGetLastError());
     return PE_OK;
 }
