@@ -25,6 +25,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-configs]
        python bench.py --copy-probe     # counter calibration: one 1 GiB copy
 """
 import argparse
+import ctypes
 import json
 import os
 import statistics
@@ -49,6 +50,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-configs", action="store_true", help="headline workload only")
     ap.add_argument("--cpu-sample-batches", type=int, default=1)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="wall-time budget of the CPU-baseline sample")
     ap.add_argument("--copy-probe", action="store_true",
                     help="run a plain 1 GiB device copy (counter calibration) and exit")
     return ap.parse_args()
@@ -166,6 +169,70 @@ def config_list():
     ]
 
 
+def transpose_list():
+    """The reference recipe's standalone operand / output transposes (Phase A
+    and Phase C of pto_einsum.h:52-177) for the BASELINE contractions that
+    have them, run through the per-shape library's run_transpose_* entry
+    points: (label, equation, operand shapes, dtype, entry point)."""
+    import torch
+
+    f16 = torch.float16
+    s3 = (4, 2048, 32, 128)
+    return [
+        ("2 in0 (0,2,1)", "bji,bjk->bik", ((16, 777, 1000), (16, 777, 1536)), torch.float32, "run_transpose_inp0"),
+        ("3 in0 (0,2,1,3)", "bshd,bthd->bsht", (s3, s3), f16, "run_transpose_inp0"),
+        ("3 in1 (0,2,3,1)", "bshd,bthd->bsht", (s3, s3), f16, "run_transpose_inp1"),
+        ("3 out (0,2,1,3)", "bshd,bthd->bsht", (s3, s3), f16, "run_transpose_out"),
+        ("5.1 in1 (1,0)", "tn,sn->ts", ((4096, 128), (4096, 128)), f16, "run_transpose_inp1"),
+    ]
+
+
+def time_transposes(dev, steps, warmup):
+    """GPU time of each standalone transpose (HIP graph replay, as for the
+    per-config figures) with its HBM roof: one read and one write of every
+    element."""
+    import torch
+
+    from pto_einsum import EinsumBuilder
+
+    rows = []
+    for label, eq, shapes, dtype, entry in transpose_list():
+        builder = EinsumBuilder(eq, [tuple(x) for x in shapes], dtype)
+        builder.build()
+        rec = builder.recipe
+        if entry == "run_transpose_out":
+            src_shape = tuple(rec["out_interpret_shape"])
+            perm = tuple(rec["out_transpose_idxs"])
+            src_dtype = torch.float32
+        else:
+            k = 0 if entry == "run_transpose_inp0" else 1
+            src_shape = tuple(builder._exec_shapes[k])
+            perm = tuple(rec["in_transpose_idxs"][k])
+            src_dtype = dtype
+        g = torch.Generator().manual_seed(7)
+        x = torch.randn(src_shape, generator=g).to(src_dtype).to(dev)
+        y = torch.empty([src_shape[p] for p in perm], dtype=src_dtype, device=dev)
+        fn = getattr(builder.lib, entry)
+
+        def run(a, b, fn=fn, x=x, y=y):
+            rc = fn(ctypes.cast(x.data_ptr(), fn.argtypes[0]), ctypes.cast(y.data_ptr(), fn.argtypes[1]),
+                    ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+            if rc != 0:
+                raise RuntimeError(f"{entry} failed ({rc})")
+
+        km = time_graph(run, None, None, max(10, steps), max(3, warmup // 2), y.numel() * y.element_size())
+        nbytes = 2 * x.numel() * x.element_size()
+        gbs = nbytes / (km * 1e-3) / 1e9
+        rows.append(dict(transpose=label, equation=eq, dtype=str(src_dtype).replace("torch.", ""),
+                         shape=list(src_shape), perm=list(perm), us=round(km * 1e3, 2), gbs=round(gbs, 1),
+                         roof="hbm", frac=round(gbs / PEAK_HBM_GBS, 4)))
+        log(f"bench: transpose {label} of {eq} {src_shape} {km * 1e3:.1f} us  {gbs:.0f} GB/s  "
+            f"hbm {gbs / PEAK_HBM_GBS * 100:.1f}%")
+        del x, y, builder
+        torch.cuda.empty_cache()
+    return rows
+
+
 def rope_table(s, d):
     import torch
 
@@ -203,8 +270,9 @@ def roofline(flops, nbytes, t_ms, dtype):
                 frac=round(gbs / PEAK_HBM_GBS, 4)), tflops, gbs
 
 
-def cpu_baseline(nbatch):
-    """Reference CPU route on `nbatch` of config 2's 16 batches, 1 thread."""
+def cpu_baseline(nbatch, budget_s=10.0, max_reps=30):
+    """Reference CPU route on `nbatch` of config 2's 16 batches, 1 thread,
+    called repeatedly for about `budget_s` seconds (median call time)."""
     import numpy as np
     import torch
 
@@ -222,14 +290,19 @@ def cpu_baseline(nbatch):
     else:
         kind = "port"
         fn = lambda: oracle.einsum(eq, a, b)  # noqa: E731
-    t = time.perf_counter()
-    fn()
-    dt = time.perf_counter() - t
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < max_reps and (time.perf_counter() - t_start) < budget_s:
+        t = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t)
+    dt = statistics.median(times)
     flops = 2.0 * nbatch * 1000 * 1536 * 777
     return dict(value=round(flops / dt / 1e12, 6), unit="TFLOP/s", cores=1, kind=kind,
                 sample=(f"{nbatch} of 16 batches of config 2 (bji,bjk->bik float32, j=777, i=1000, "
-                        f"k=1536): {flops / 1e9:.2f} GFLOP in {dt:.2f} s on 1 thread of {os.cpu_count()}"),
-                seconds=round(dt, 3))
+                        f"k=1536), {flops / 1e9:.2f} GFLOP per call, called {len(times)} times "
+                        f"({sum(times):.1f} s); median call {dt:.3f} s on 1 thread of {os.cpu_count()}"),
+                seconds=round(sum(times), 3))
 
 
 def main():
@@ -287,8 +360,10 @@ def main():
             del x, y, r
             torch.cuda.empty_cache()
 
+    transposes = [] if args.no_configs else time_transposes(dev, args.steps, args.warmup)
+
     log("bench: timing the CPU baseline")
-    cpu = cpu_baseline(args.cpu_sample_batches)
+    cpu = cpu_baseline(args.cpu_sample_batches, args.cpu_seconds)
     log(f"bench: cpu baseline {cpu}")
 
     line = {
@@ -309,6 +384,7 @@ def main():
         "roofline": roof,
         "cpu_baseline": cpu,
         "per_config": per_config,
+        "transposes": transposes,
     }
     print(json.dumps(line), flush=True)
 

@@ -65,6 +65,10 @@ GemmChoice choose(const pe_gemm_desc& d) {
     c.persist = PE_GEMM_PERSIST;
     if (d.tile == 64 || d.tile == 128) {
         c.bm = c.bn = d.tile;
+    } else if (d.tile == 256) {
+        c.bm = d.M >= d.N ? 256 : 128;
+        c.bn = d.M >= d.N ? 128 : 256;
+        c.persist = PE_GEMM_BIG_PERSIST;
     } else {
         c.bm = (d.M > 64 && d.N > 64) ? 128 : 64;
         if (c.bm == 128 && c.nbatch_total * ceil_div(d.M, 128) * ceil_div(d.N, 128) < cus) c.bm = 64;
@@ -126,6 +130,9 @@ int validate_gemm(const pe_gemm_desc& d) {
     if (d.dtype != PE_F32 && d.dtype != PE_F16)
         return fail(PE_ERR_UNSUPPORTED, "gemm: dtype must be PE_F32 or PE_F16");
     if (d.nbatch < 0 || d.nbatch > PE_MAX_DIMS) return fail(PE_ERR_INVALID, "gemm: nbatch out of range");
+    if (d.tile != 0 && d.tile != 64 && d.tile != 128 && d.tile != 256)
+        return fail(PE_ERR_INVALID, "gemm: tile must be 0, 64, 128 or 256");
+    if (d.split_k < 0) return fail(PE_ERR_INVALID, "gemm: split_k must be >= 0");
     if (d.M < 0 || d.N < 0 || d.K < 0) return fail(PE_ERR_INVALID, "gemm: negative extent");
     if (d.M >= (int64_t(1) << 31) || d.N >= (int64_t(1) << 31) || d.K >= (int64_t(1) << 31))
         return fail(PE_ERR_UNSUPPORTED, "gemm: M, N and K must each be below 2^31");

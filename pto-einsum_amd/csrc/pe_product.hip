@@ -37,8 +37,11 @@
 #ifndef PE_PRODUCT_UNROLL
 #define PE_PRODUCT_UNROLL 1
 #endif
-#ifndef PE_PRODUCT_VEC
-#define PE_PRODUCT_VEC 4
+#ifndef PE_PRODUCT_VEC_F32
+#define PE_PRODUCT_VEC_F32 4
+#endif
+#ifndef PE_PRODUCT_VEC_F16
+#define PE_PRODUCT_VEC_F16 4
 #endif
 
 namespace pe {
@@ -296,7 +299,7 @@ int run(const pe_product_desc& d, const void* in0, const void* in1, float* out,
     // store covers 1 KB contiguously (float16 inputs load 8 bytes per lane).
     // Needs a unit inner stride, an inner extent and outer strides that are
     // whole vectors, and vector-aligned base pointers.
-    constexpr int VEC = PE_PRODUCT_VEC;
+    constexpr int VEC = E::kBytes == 4 ? PE_PRODUCT_VEC_F32 : PE_PRODUCT_VEC_F16;
     constexpr size_t VB = size_t(VEC) * E::kBytes;
     bool vec_ok = nd > 0 && args.a_inner == 1 && (args.b_inner == 0 || args.b_inner == 1) &&
                   inner % VEC == 0 && aligned(in0, VB) && aligned(out, 16) &&
