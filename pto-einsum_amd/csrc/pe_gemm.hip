@@ -18,6 +18,11 @@
 #ifndef PE_GEMM_BIG_PERSIST
 #define PE_GEMM_BIG_PERSIST 0
 #endif
+// Smallest slot fill (tiles / (rounds * resident slots)) at which the
+// 256-wide float32 tiles are taken.
+#ifndef PE_GEMM_BIG_MIN_FILL
+#define PE_GEMM_BIG_MIN_FILL 0.95
+#endif
 
 namespace pe {
 
@@ -65,20 +70,23 @@ GemmChoice choose(const pe_gemm_desc& d) {
     c.persist = PE_GEMM_PERSIST;
     if (d.tile == 64 || d.tile == 128) {
         c.bm = c.bn = d.tile;
-    } else if (d.tile == 256) {
-        c.bm = d.M >= d.N ? 256 : 128;
-        c.bn = d.M >= d.N ? 128 : 256;
+    } else if (d.tile == 192 || d.tile == 256) {
+        c.bm = d.M >= d.N ? d.tile : 128;
+        c.bn = d.M >= d.N ? 128 : d.tile;
         c.persist = PE_GEMM_BIG_PERSIST;
     } else {
         c.bm = (d.M > 64 && d.N > 64) ? 128 : 64;
         if (c.bm == 128 && c.nbatch_total * ceil_div(d.M, 128) * ceil_div(d.N, 128) < cus) c.bm = 64;
         c.bn = c.bm;
         if (PE_GEMM_BIG && c.bm == 128 && d.dtype == PE_F32) {
-            // 256x128 tiles halve the fragment reads per MFMA but hold only
-            // two waves per SIMD.  Pick the tiling whose tiles fill the
-            // resident slots most evenly; the larger tile gets the ~12 % edge
-            // measured on large square problems.
-            auto util = [&](int bm, int bn) {
+            // 256x128 / 128x256 tiles (wave tile 128x64) read fewer LDS
+            // fragments per MFMA but hold two waves per SIMD.  Measured on
+            // MI355X: they beat 128x128 by 10-25 % when their tiles fill the
+            // resident block slots in whole rounds (4096^2 at K = 512..4096),
+            // and lose by 5-35 % when a round is left part-filled (config 2:
+            // 1.5 rounds, where the last round runs one block per CU).  So
+            // take them only for (nearly) whole rounds.
+            auto fill = [&](int bm, int bn) {
                 const int64_t t = c.nbatch_total * ceil_div(d.M, bm) * ceil_div(d.N, bn);
                 const int64_t slots = cus * gemm_occupancy_f32(bm, bn);
                 const int64_t rounds = ceil_div(t, slots);
@@ -87,7 +95,7 @@ GemmChoice choose(const pe_gemm_desc& d) {
             const bool tall = d.M >= d.N;
             const int bbm = tall ? 256 : 128, bbn = tall ? 128 : 256;
             const int64_t bt = c.nbatch_total * ceil_div(d.M, bbm) * ceil_div(d.N, bbn);
-            if (bt >= cus && util(bbm, bbn) * 1.12 > util(128, 128)) {
+            if (bt >= cus && fill(bbm, bbn) >= PE_GEMM_BIG_MIN_FILL) {
                 c.bm = bbm;
                 c.bn = bbn;
                 c.persist = PE_GEMM_BIG_PERSIST;
@@ -130,8 +138,10 @@ int validate_gemm(const pe_gemm_desc& d) {
     if (d.dtype != PE_F32 && d.dtype != PE_F16)
         return fail(PE_ERR_UNSUPPORTED, "gemm: dtype must be PE_F32 or PE_F16");
     if (d.nbatch < 0 || d.nbatch > PE_MAX_DIMS) return fail(PE_ERR_INVALID, "gemm: nbatch out of range");
-    if (d.tile != 0 && d.tile != 64 && d.tile != 128 && d.tile != 256)
-        return fail(PE_ERR_INVALID, "gemm: tile must be 0, 64, 128 or 256");
+    if (d.tile != 0 && d.tile != 64 && d.tile != 128 && d.tile != 192 && d.tile != 256)
+        return fail(PE_ERR_INVALID, "gemm: tile must be 0, 64, 128, 192 or 256");
+    if (d.tile == 192 && d.dtype != PE_F32)
+        return fail(PE_ERR_UNSUPPORTED, "gemm: the 192 tile is float32 only");
     if (d.split_k < 0) return fail(PE_ERR_INVALID, "gemm: split_k must be >= 0");
     if (d.M < 0 || d.N < 0 || d.K < 0) return fail(PE_ERR_INVALID, "gemm: negative extent");
     if (d.M >= (int64_t(1) << 31) || d.N >= (int64_t(1) << 31) || d.K >= (int64_t(1) << 31))

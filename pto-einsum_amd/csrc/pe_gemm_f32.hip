@@ -53,15 +53,20 @@ static int occ() {
 }
 
 int gemm_occupancy_f32(int bm, int bn) {
-    static const int o[4] = {occ<64, 64>(), occ<128, 128>(), occ<256, 128>(), occ<128, 256>()};
+    static const int o[6] = {occ<64, 64>(),   occ<128, 128>(), occ<256, 128>(),
+                             occ<128, 256>(), occ<192, 128>(), occ<128, 192>()};
     if (bm == 256) return o[2];
     if (bn == 256) return o[3];
+    if (bm == 192) return o[4];
+    if (bn == 192) return o[5];
     return bm == 128 ? o[1] : o[0];
 }
 
 hipError_t launch_gemm_f32(int bm, int bn, int al, int bl, const GemmArgs& g, hipStream_t s) {
     if (bm == 256) return go_a<256, 128>(al, bl, g, s);
     if (bn == 256) return go_a<128, 256>(al, bl, g, s);
+    if (bm == 192) return go_a<192, 128>(al, bl, g, s);
+    if (bn == 192) return go_a<128, 192>(al, bl, g, s);
     return bm == 128 ? go_a<128, 128>(al, bl, g, s) : go_a<64, 64>(al, bl, g, s);
 }
 

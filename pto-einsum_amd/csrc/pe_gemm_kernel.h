@@ -65,6 +65,10 @@ template <typename E, int ROWS, int BK, int LD, bool KC, int LAYOUT, int NV>
 struct TileLoader {
     using T = typename E::T;
     static constexpr int VEC = 16 / E::kBytes;
+    // L_MN: whole row chunks per thread when the threads split evenly over
+    // the vectors of one k row; else a strided vector walk (k-major LDS only).
+    static constexpr bool kRowChunks = kGemmThreads % (ROWS / VEC) == 0;
+    static_assert(LAYOUT != L_MN || kRowChunks || !KC, "strided L_MN walk needs k-major LDS");
     T stage[NV][VEC];
 
     __device__ __forceinline__ static void vload(const T* p, T (&d)[VEC]) {
@@ -78,7 +82,26 @@ struct TileLoader {
     // rows_left/k_left: valid extent from the tile origin.
     __device__ __forceinline__ void load(const T* __restrict__ base, int64_t rs, int64_t ks,
                                          int rows_left, int k_left, int tid) {
-        if constexpr (LAYOUT == L_MN) {
+        if constexpr (LAYOUT == L_MN && !kRowChunks) {
+            // Rows that do not divide the block: vector idx = tid + v*threads
+            // covers (k = idx / VPR, rows (idx % VPR)*VEC ..).
+            constexpr int VPR = ROWS / VEC;
+#pragma unroll
+            for (int v = 0; v < NV; ++v) {
+                const int idx = tid + v * kGemmThreads;
+                const int k = idx / VPR, r = (idx % VPR) * VEC;
+                if (k >= k_left) {
+#pragma unroll
+                    for (int j = 0; j < VEC; ++j) stage[v][j] = T(0);
+                } else if (r + VEC <= rows_left) {
+                    vload(base + int64_t(k) * ks + r, stage[v]);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < VEC; ++j)
+                        stage[v][j] = base[int64_t(k) * ks + min(r + j, rows_left - 1)];
+                }
+            }
+        } else if constexpr (LAYOUT == L_MN) {
             constexpr int VPR = ROWS / VEC;
             const int r = (tid % VPR) * VEC;
             const int k0 = (tid / VPR) * NV;
@@ -121,7 +144,19 @@ struct TileLoader {
     }
 
     __device__ __forceinline__ void store(T* lds, int tid) const {
-        if constexpr (LAYOUT == L_MN) {
+        if constexpr (LAYOUT == L_MN && !kRowChunks) {
+            constexpr int VPR = ROWS / VEC;
+            using V = typename Pack<VEC, T>::type;
+#pragma unroll
+            for (int v = 0; v < NV; ++v) {
+                const int idx = tid + v * kGemmThreads;
+                const int k = idx / VPR, r = (idx % VPR) * VEC;
+                V x;
+#pragma unroll
+                for (int j = 0; j < VEC; ++j) x[j] = stage[v][j];
+                *reinterpret_cast<V*>(lds + k * LD + r) = x;
+            }
+        } else if constexpr (LAYOUT == L_MN) {
             constexpr int VPR = ROWS / VEC;
             const int r = (tid % VPR) * VEC;
             const int k0 = (tid / VPR) * NV;
@@ -200,13 +235,16 @@ struct TileWalk {
 #ifndef PE_GEMM_PRELOAD
 #define PE_GEMM_PRELOAD -1
 #endif
+#ifndef PE_GEMM_PRELOAD_MIN
+#define PE_GEMM_PRELOAD_MIN (256 * 128)
+#endif
 
 
 template <typename E, int BM, int BN, int BK, bool KC, int NBUF, int ALAYOUT, int BLAYOUT>
 __global__ __launch_bounds__(kGemmThreads, 2) void gemm_kernel(GemmArgs g) {
     using G = GemmGeom<E, BM, BN, BK, KC, NBUF>;
     using T = typename E::T;
-    constexpr int PRELOAD = PE_GEMM_PRELOAD >= 0 ? PE_GEMM_PRELOAD : (BM * BN >= 256 * 128 ? 1 : 0);
+    constexpr int PRELOAD = PE_GEMM_PRELOAD >= 0 ? PE_GEMM_PRELOAD : (BM * BN >= PE_GEMM_PRELOAD_MIN ? 1 : 0);
     __shared__ __attribute__((aligned(16))) T lds_a[NBUF][G::A_ELEMS];
     __shared__ __attribute__((aligned(16))) T lds_b[NBUF][G::B_ELEMS];
 

@@ -110,3 +110,66 @@ def test_staged_plans_on_gpu(eq, s0, s1, dtype, build_dir):
     got = einsum(eq, a.cuda(), b.cuda()).cpu().numpy()
     want = oracle.einsum(eq, a.float().numpy(), b.float().numpy())
     check(got, want, contraction_size(eq, s0, s1) <= 1, RTOL[dtype], eq)
+
+
+def _gemm_direct(a, b, M, N, K, a_ms, a_ks, b_ks, b_ns, dtype_code, tile=0, split_k=0, nbatch=2):
+    """C[bt] = A[bt] @ B[bt] through pe_gemm with explicit strides; A and B are
+    flat device buffers holding `nbatch` operands each."""
+    lib = abi.bind()
+    a_bs = (M - 1) * a_ms + (K - 1) * a_ks + 1
+    b_bs = (N - 1) * b_ns + (K - 1) * b_ks + 1
+    d = launch.GemmDesc(dtype=dtype_code, batch_shape=[nbatch], a_bstride=[a_bs], b_bstride=[b_bs],
+                        c_bstride=[M * N], M=M, N=N, K=K, a_ms=a_ms, a_ks=a_ks, b_ks=b_ks, b_ns=b_ns,
+                        c_ms=N, c_ns=1, a_numel=a.numel(), b_numel=b.numel(), c_numel=nbatch * M * N,
+                        split_k=split_k, tile=tile)
+    cd = abi.gemm_desc(d)
+    ws_bytes = lib.pe_gemm_workspace_bytes(ctypes.byref(cd))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device="cuda")
+    c = torch.empty(nbatch * M * N, dtype=torch.float32, device="cuda")
+    rc = lib.pe_gemm(ctypes.byref(cd), _ptr(a), _ptr(b), ctypes.c_void_p(c.data_ptr()), _ptr(ws),
+                     ws_bytes, _stream())
+    assert rc == 0, runtime.last_error()
+    return c.cpu().reshape(nbatch, M, N)
+
+
+@pytest.mark.parametrize("tile,dtype", [(64, torch.float32), (128, torch.float32), (192, torch.float32),
+                                        (256, torch.float32), (64, torch.float16), (128, torch.float16),
+                                        (256, torch.float16)])
+@pytest.mark.parametrize("M,N,K", [(300, 200, 77), (200, 300, 77), (390, 390, 33),
+                                   (264, 136, 40), (136, 264, 40)])
+@pytest.mark.parametrize("layout", ["mn", "k"])
+@pytest.mark.parametrize("split_k", [0, 3])
+def test_gemm_tiles_direct(tile, dtype, M, N, K, layout, split_k):
+    """Every tile shape in both orientations (M >= N picks the tall variant),
+    both vector loaders (rows contiguous / k contiguous), partial tiles in M,
+    N and K, with and without split-K, against a float64 reference."""
+    nbatch = 2
+    g = torch.Generator().manual_seed(M * 7 + N + K)
+    A = torch.randn(nbatch, M, K, generator=g).to(dtype)
+    B = torch.randn(nbatch, K, N, generator=g).to(dtype)
+    if layout == "mn":    # A stored [K][M] (m contiguous), B stored [K][N] (n contiguous)
+        a_buf, a_ms, a_ks = A.transpose(1, 2).contiguous(), 1, M
+        b_buf, b_ks, b_ns = B.contiguous(), N, 1
+    else:                 # A stored [M][K], B stored [N][K] (k contiguous)
+        a_buf, a_ms, a_ks = A.contiguous(), K, 1
+        b_buf, b_ks, b_ns = B.transpose(1, 2).contiguous(), 1, K
+    code = launch.DT_F32 if dtype == torch.float32 else launch.DT_F16
+    got = _gemm_direct(a_buf.reshape(-1).cuda(), b_buf.reshape(-1).cuda(), M, N, K, a_ms, a_ks, b_ks, b_ns,
+                       code, tile=tile, split_k=split_k, nbatch=nbatch)
+    want = torch.bmm(A.double(), B.double()).numpy()
+    scale = float(np.abs(want).max())
+    rtol = 1e-4 if dtype == torch.float32 else 2e-3
+    assert float(np.abs(got.numpy() - want).max()) <= rtol * scale
+
+
+def test_gemm_rejects_bad_tile():
+    lib = abi.bind()
+    d = launch.GemmDesc(dtype=launch.DT_F16, batch_shape=[1], a_bstride=[0], b_bstride=[0], c_bstride=[0],
+                        M=4, N=4, K=4, a_ms=4, a_ks=1, b_ks=4, b_ns=1, c_ms=4, c_ns=1, a_numel=16,
+                        b_numel=16, c_numel=16, tile=192)
+    x = torch.zeros(16, device="cuda")
+    rc = lib.pe_gemm(ctypes.byref(abi.gemm_desc(d)), _ptr(x), _ptr(x), _ptr(x), None, 0, _stream())
+    assert rc == -3 and "192" in runtime.last_error()
+    d.tile, d.dtype = 96, launch.DT_F32
+    rc = lib.pe_gemm(ctypes.byref(abi.gemm_desc(d)), _ptr(x), _ptr(x), _ptr(x), None, 0, _stream())
+    assert rc == -1 and "tile" in runtime.last_error()

@@ -118,10 +118,11 @@ def test_config5_rope_broadcast():
     check(got, oracle.einsum("bshd,sd->bshd", x.float().numpy(), c.float().numpy()), True, 0, "5.R")
 
 
-@pytest.mark.parametrize("s0,s1", [((4096, 1024), (1024, 4096)),      # 256x128 tiles, full
-                                   ((2000, 777), (777, 4100)),        # 128x256 tiles, partial, K tail
-                                   ((4000, 300), (300, 2200))])       # 256x128, partial in M and N
+@pytest.mark.parametrize("s0,s1", [((4096, 1024), (1024, 4096)),      # 256x128 tiles in whole rounds
+                                   ((2000, 777), (777, 4100)),        # 128x128, partial, K tail
+                                   ((4000, 300), (300, 2200))])       # 128x128, partial in M and N
 def test_large_fp32_gemm_tilings(s0, s1):
-    """Shapes whose tile grids select the 256x128 / 128x256 tiles."""
+    """Large float32 GEMMs through the automatic tile choice (every tile
+    shape is also forced directly in test_gpu_components)."""
     g = torch.Generator().manual_seed(8)
     _contraction("ij,jk->ik", torch.randn(s0, generator=g), torch.randn(s1, generator=g), 1e-4, samples=2048)
