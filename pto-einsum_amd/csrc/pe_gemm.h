@@ -82,7 +82,11 @@ int gemm_bk(int dtype);
 // returns resident blocks per CU of that tile (runtime occupancy query).
 int gemm_occupancy_f32(int bm, int bn);
 int gemm_occupancy_f16(int bm, int bn);
-hipError_t launch_gemm_f32(int bm, int bn, int alayout, int blayout, const GemmArgs& g, hipStream_t s);
-hipError_t launch_gemm_f16(int bm, int bn, int alayout, int blayout, const GemmArgs& g, hipStream_t s);
+// persist: 0 = one block per tile; > 0 = at most that many blocks per CU;
+// < 0 = as many blocks per CU as the launched kernel keeps resident.
+hipError_t launch_gemm_f32(int bm, int bn, int alayout, int blayout, int persist, const GemmArgs& g,
+                           hipStream_t s);
+hipError_t launch_gemm_f16(int bm, int bn, int alayout, int blayout, int persist, const GemmArgs& g,
+                           hipStream_t s);
 
 }  // namespace pe

@@ -5,10 +5,10 @@
 
 #include <algorithm>
 
-// Resident blocks per CU when the tile loop is persistent; 0 launches one
-// block per tile.
+// Blocks per CU of the persistent tile loop: 0 launches one block per tile,
+// -1 as many blocks as the launched kernel keeps resident per CU.
 #ifndef PE_GEMM_PERSIST
-#define PE_GEMM_PERSIST 0
+#define PE_GEMM_PERSIST -1
 #endif
 // 256x128 / 128x256 tiles (wave tile 128x64) for grids that still fill the
 // GPU, with their own persistent block count.
@@ -16,7 +16,7 @@
 #define PE_GEMM_BIG 1
 #endif
 #ifndef PE_GEMM_BIG_PERSIST
-#define PE_GEMM_BIG_PERSIST 0
+#define PE_GEMM_BIG_PERSIST -1
 #endif
 // Smallest slot fill (tiles / (rounds * resident slots)) at which the
 // 256-wide float32 tiles are taken.
@@ -49,7 +49,7 @@ namespace {
 
 struct GemmChoice {
     int bm, bn;    // tile: 64x64, 128x128, 256x128 or 128x256
-    int persist;   // blocks per CU of a persistent grid (0: one block per tile)
+    int persist;   // blocks per CU of a persistent grid (0: one block per tile, -1: resident count)
     int nsplit;    // K splits (1 = direct store)
     int k_per_split;
     int64_t nbatch_total;
@@ -239,10 +239,6 @@ extern "C" int pe_gemm(const pe_gemm_desc* d, const void* a, const void* b, floa
     g.total_blocks = g.tiles_per_batch * g.nbatch_total * uint32_t(ch.nsplit);
     g.grid = g.total_blocks;
     g.store_nt = (ch.nsplit > 1 ? ch.ws_bytes : nb * d->M * d->N * 4) >= PE_NT_MIN_BYTES;
-    if (ch.persist > 0) {
-        const uint32_t cap = uint32_t(cu_count()) * uint32_t(ch.persist);
-        if (g.grid > cap) g.grid = cap;
-    }
     g.a_ms = d->a_ms; g.a_ks = d->a_ks; g.b_ks = d->b_ks; g.b_ns = d->b_ns;
     g.c_ms = d->c_ms; g.c_ns = d->c_ns;
     g.nbatch = d->nbatch;
@@ -252,8 +248,8 @@ extern "C" int pe_gemm(const pe_gemm_desc* d, const void* a, const void* b, floa
         g.b_bs[i] = d->b_bstride[i];
         g.c_bs[i] = d->c_bstride[i];
     }
-    hipError_t e = d->dtype == PE_F32 ? launch_gemm_f32(ch.bm, ch.bn, al, bl, g, s)
-                                      : launch_gemm_f16(ch.bm, ch.bn, al, bl, g, s);
+    hipError_t e = d->dtype == PE_F32 ? launch_gemm_f32(ch.bm, ch.bn, al, bl, ch.persist, g, s)
+                                      : launch_gemm_f16(ch.bm, ch.bn, al, bl, ch.persist, g, s);
     PE_CHECK_HIP(e);
     if (ch.nsplit > 1) {
         r.nsplit = ch.nsplit;

@@ -254,36 +254,60 @@ __global__ __launch_bounds__(kGemmThreads, 2) void gemm_kernel(GemmArgs g) {
     const int wm = wave >> 1, wn = wave & 1;
     const uint32_t tiles_all = g.tiles_per_batch * g.nbatch_total;
 
-    TileWalk walk(g.total_blocks);
-    for (uint32_t bid = walk.next; bid < walk.end; bid += walk.step) {
-        const uint32_t split = bid / tiles_all;
-        uint32_t t = bid - split * tiles_all;
-        const uint32_t batch = t / g.tiles_per_batch;
-        t -= batch * g.tiles_per_batch;
+    // Operand origins and extents of one tile (split, batch, tm, tn).
+    struct Tile {
+        const T* A;
+        const T* B;
+        int64_t c_off;
+        uint32_t split, batch;
+        int m0, n0, rows_a, rows_b, k_len;
+    };
+    auto locate = [&](uint32_t bid) {
+        Tile x;
+        x.split = bid / tiles_all;
+        uint32_t t = bid - x.split * tiles_all;
+        x.batch = t / g.tiles_per_batch;
+        t -= x.batch * g.tiles_per_batch;
         const int tm = int(t / uint32_t(g.tiles_n));
         const int tn = int(t - uint32_t(tm) * uint32_t(g.tiles_n));
-
         int64_t a_off = 0, b_off = 0, c_off = 0;
-        {
-            uint32_t rem = batch;
-            for (int d = g.nbatch - 1; d >= 0; --d) {
-                uint32_t q, r;
-                g.batch_div[d].divmod(rem, q, r);
-                a_off += int64_t(r) * g.a_bs[d];
-                b_off += int64_t(r) * g.b_bs[d];
-                c_off += int64_t(r) * g.c_bs[d];
-                rem = q;
-            }
+        uint32_t rem = x.batch;
+        for (int d = g.nbatch - 1; d >= 0; --d) {
+            uint32_t q, r;
+            g.batch_div[d].divmod(rem, q, r);
+            a_off += int64_t(r) * g.a_bs[d];
+            b_off += int64_t(r) * g.b_bs[d];
+            c_off += int64_t(r) * g.c_bs[d];
+            rem = q;
         }
-        const int m0 = tm * BM, n0 = tn * BN;
-        const int kb = int(split) * g.k_per_split;
-        const int ke = min(g.K, kb + g.k_per_split);
-        const int rows_a = g.M - m0, rows_b = g.N - n0;
-        const T* __restrict__ A = static_cast<const T*>(g.a) + a_off + int64_t(m0) * g.a_ms + int64_t(kb) * g.a_ks;
-        const T* __restrict__ B = static_cast<const T*>(g.b) + b_off + int64_t(n0) * g.b_ns + int64_t(kb) * g.b_ks;
+        x.m0 = tm * BM;
+        x.n0 = tn * BN;
+        const int kb = int(x.split) * g.k_per_split;
+        x.k_len = min(g.K, kb + g.k_per_split) - kb;
+        x.rows_a = g.M - x.m0;
+        x.rows_b = g.N - x.n0;
+        x.A = static_cast<const T*>(g.a) + a_off + int64_t(x.m0) * g.a_ms + int64_t(kb) * g.a_ks;
+        x.B = static_cast<const T*>(g.b) + b_off + int64_t(x.n0) * g.b_ns + int64_t(kb) * g.b_ks;
+        x.c_off = c_off;
+        return x;
+    };
 
-        TileLoader<E, BM, BK, G::A_LD, KC, ALAYOUT, G::A_VECS> la;
-        TileLoader<E, BN, BK, G::B_LD, KC, BLAYOUT, G::B_VECS> lb;
+    TileLoader<E, BM, BK, G::A_LD, KC, ALAYOUT, G::A_VECS> la;
+    TileLoader<E, BN, BK, G::B_LD, KC, BLAYOUT, G::B_VECS> lb;
+
+    TileWalk walk(g.total_blocks);
+    uint32_t bid = walk.next;
+    if (bid >= walk.end) return;
+    Tile cur_t = locate(bid);
+    la.load(cur_t.A, g.a_ms, g.a_ks, cur_t.rows_a, cur_t.k_len, tid);
+    lb.load(cur_t.B, g.b_ns, g.b_ks, cur_t.rows_b, cur_t.k_len, tid);
+    for (;;) {
+        const T* __restrict__ A = cur_t.A;
+        const T* __restrict__ B = cur_t.B;
+        const int m0 = cur_t.m0, n0 = cur_t.n0;
+        const int rows_a = cur_t.rows_a, rows_b = cur_t.rows_b;
+        const uint32_t split = cur_t.split, batch = cur_t.batch;
+        const int64_t c_off = cur_t.c_off;
 
         f32x16 acc[G::FM][G::FN];
 #pragma unroll
@@ -293,10 +317,8 @@ __global__ __launch_bounds__(kGemmThreads, 2) void gemm_kernel(GemmArgs g) {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-        const int nslabs = (ke - kb + BK - 1) / BK;
-        int k_left = ke - kb;
-        la.load(A, g.a_ms, g.a_ks, rows_a, k_left, tid);
-        lb.load(B, g.b_ns, g.b_ks, rows_b, k_left, tid);
+        const int nslabs = (cur_t.k_len + BK - 1) / BK;
+        int k_left = cur_t.k_len;
         la.store(lds_a[0], tid);
         lb.store(lds_b[0], tid);
         __syncthreads();
@@ -435,6 +457,14 @@ __global__ __launch_bounds__(kGemmThreads, 2) void gemm_kernel(GemmArgs g) {
                 }
             }
         }
+        // Next tile of a persistent block.  (Loading its first slab before
+        // this epilogue instead measured slower: the extra live registers
+        // cost a resident block per CU.)
+        bid += walk.step;
+        if (bid >= walk.end) break;
+        cur_t = locate(bid);
+        la.load(cur_t.A, g.a_ms, g.a_ks, cur_t.rows_a, cur_t.k_len, tid);
+        lb.load(cur_t.B, g.b_ns, g.b_ks, cur_t.rows_b, cur_t.k_len, tid);
     }
 }
 

@@ -165,7 +165,8 @@ __global__ __launch_bounds__(kThreads) void tile_transpose_kernel(TileArgs p) {
         const int64_t p0 = int64_t(tp) * kTile, q0 = int64_t(tq) * kTile;
         // Read: tile rows are q, each lane covers LW consecutive p.
 #pragma unroll
-        for (int r = lr; r < kTile; r += kThreads / LVPR) {
+        for (int it = 0; it < kTile / (kThreads / LVPR); ++it) {
+            const int r = lr + it * (kThreads / LVPR);
             const int64_t gq = q0 + r, gp = p0 + lc * LW;
             if (gq >= p.Q) continue;
             const W* s = src + sbase + gq * p.src_q_stride + gp;
@@ -182,7 +183,8 @@ __global__ __launch_bounds__(kThreads) void tile_transpose_kernel(TileArgs p) {
         __syncthreads();
         // Write: destination rows are p, each lane covers SW consecutive q.
 #pragma unroll
-        for (int r = sr; r < kTile; r += kThreads / SVPR) {
+        for (int it = 0; it < kTile / (kThreads / SVPR); ++it) {
+            const int r = sr + it * (kThreads / SVPR);
             const int64_t gp = p0 + r, gq = q0 + sc * SW;
             if (gp >= p.P) continue;
             W* d = dst + dbase + gp * p.dst_p_stride + gq;
