@@ -233,6 +233,38 @@ def time_transposes(dev, steps, warmup):
     return rows
 
 
+def time_fused_chain(dev, steps, warmup):
+    """BASELINE config 5's linear-attention chain in one fused launch
+    (pto_einsum.linear_attention): q, k float16 normal(0, 1/sqrt(128)), v
+    float16 normal(0, 1) (read as float32), the causal decay mask
+    gamma^(t-s), gamma = 0.995, in float32; t = s = 4096, n = p = 128.  The
+    roof is the MFMA time of the chain's dense work: 2*T*S*N flops at the
+    float16 peak plus 2*T*S*P at the float32 peak (T*S mask multiplies on the
+    VALU are not counted against it).  Blocks of the mask that are zero are
+    skipped, so the causal case can beat the dense roof in principle."""
+    import torch
+
+    from pto_einsum import linear_attention
+
+    T = S = 4096
+    N = P = 128
+    g = torch.Generator().manual_seed(105)
+    q = (torch.randn(T, N, generator=g) * N ** -0.5).half().to(dev)
+    k = (torch.randn(S, N, generator=g) * N ** -0.5).half().to(dev)
+    v = torch.randn(S, P, generator=g).half().to(dev)
+    i = torch.arange(T, dtype=torch.float64)
+    d = i[:, None] - i[None, :]
+    m = torch.where(d >= 0, 0.995 ** d.clamp(min=0), torch.zeros(())).float().to(dev)
+    km = time_graph(lambda a, b: linear_attention(q, k, v, m), None, None, max(10, steps), max(3, warmup // 2),
+                    T * P * 4)
+    flops = 2 * T * S * N + T * S + 2 * T * S * P
+    nbytes = (q.numel() + k.numel() + v.numel()) * 2 + m.numel() * 4 + T * P * 4
+    floor_ms = (2 * T * S * P / (PEAK_TFLOPS["f32"] * 1e12) + 2 * T * S * N / (PEAK_TFLOPS["f16"] * 1e12)) * 1e3
+    return dict(config="5.F", equation="tn,sn,sp,ts->tp (fused)", dtype="f16/f32", us=round(km * 1e3, 2),
+                tflops=round(flops / (km * 1e-3) / 1e12, 3), gbs=round(nbytes / (km * 1e-3) / 1e9, 1),
+                roof="mfma", frac=round(floor_ms / km, 4))
+
+
 def rope_table(s, d):
     import torch
 
@@ -359,6 +391,14 @@ def main():
                 f"{rf['bound']} {rf['frac'] * 100:.1f}%")
             del x, y, r
             torch.cuda.empty_cache()
+
+    if not args.no_configs:
+        fused = time_fused_chain(dev, args.steps, args.warmup)
+        chain_us = sum(c["us"] for c in per_config if c["config"] in ("5.1", "5.2", "5.3"))
+        fused["three_einsums_us"] = round(chain_us, 2)
+        per_config.append(fused)
+        log(f"bench: config 5 fused tn,sn,sp,ts->tp {fused['us']:.1f} us ({fused['tflops']:.1f} TFLOP/s "
+            f"dense-equivalent, mfma {fused['frac'] * 100:.1f}%); the three einsums take {chain_us:.1f} us")
 
     transposes = [] if args.no_configs else time_transposes(dev, args.steps, args.warmup)
 

@@ -114,6 +114,34 @@ int64_t pe_gemm_workspace_bytes(const pe_gemm_desc* d);
 int pe_gemm(const pe_gemm_desc* d, const void* a, const void* b, float* c, void* ws,
             int64_t ws_bytes, void* stream);
 
+/* Fused linear-attention chain.  No single entry point of the reference
+ * corresponds: it runs the chain as three einsums with float32 intermediates
+ * (tests/test_llm_ops.py:81-107, benchmarks/complex/bench_linear_attention.py:62-94):
+ *   A = einsum("tn,sn->ts", q, k); A = einsum("ts,ts->ts", A, m);
+ *   out = einsum("ts,sp->tp", A, v).
+ * This launches it as one kernel (plus a split reduction when the workspace
+ * is used): out[t,p] = sum_s ((sum_n q[t,n] k[s,n]) * m[t,s]) * v[s,p], every
+ * operand read as float32 (float16 up-cast exactly), the inner sum and the
+ * mask product rounded to float32 as in the three-step chain.  Rows of q, k,
+ * v and m are contiguous with the given row strides; out is [T][P] float32.
+ * N <= 256 for float16 q/k, N <= 128 for float32.  The workspace holds split
+ * partials and zero-padded copies of q / k / m when their rows are not whole
+ * 16-byte (q, k) or 4-element (m) vectors; the size query assumes 16-byte
+ * aligned base addresses (a misaligned base needs a padded copy too). */
+typedef struct pe_linattn_desc {
+    int32_t qk_dtype;                   /* element type of q and k */
+    int32_t v_dtype;
+    int32_t m_dtype;
+    int32_t split;                      /* 0 = choose; else number of s splits */
+    int64_t T, S, N, P;
+    int64_t q_ts, k_ss, v_ss, m_ts;     /* row strides, in elements */
+    int64_t q_numel, k_numel, v_numel, m_numel;
+} pe_linattn_desc;
+
+int64_t pe_linear_attention_workspace_bytes(const pe_linattn_desc* d);
+int pe_linear_attention(const pe_linattn_desc* d, const void* q, const void* k, const void* v,
+                        const void* m, float* out, void* ws, int64_t ws_bytes, void* stream);
+
 /* Plan executor: the body of every per-shape run_einsum_exec. */
 int pe_einsum_exec(const pe_einsum_plan* p, const void* in0, const void* in1, float* out,
                    void* ws, void* stream);

@@ -18,6 +18,9 @@ Pieces and the reference code each one follows:
   defined on the up-cast values.
 * ``sampled``      -- the same per-output sum for selected outputs only,
   addressed in the raw operands; bit-identical to ``einsum`` there.
+* ``linear_attention`` -- the reference's three-einsum linear-attention chain
+  (tests/test_llm_ops.py:81-107) composed from ``einsum``, float32
+  intermediates.
 
 Parity pins: tests/test_oracle.py checks each piece against oracle/_ref (the
 reference header compiled from /root/reference when present), the committed
@@ -182,6 +185,14 @@ def transpose(x, perm):
 def einsum(eq, a, b):
     """The reference CPU route's result for ``eq`` on float32 (or up-cast) inputs."""
     a, b = _as_f32(a), _as_f32(b)
+    lhs = eq.replace(" ", "").split("->")[0].split(",")
+    sizes = {}
+    for labels, shape in ((lhs[0], a.shape), (lhs[1], b.shape)):
+        if len(labels) != len(shape):
+            raise ValueError(f"oracle einsum: {labels!r} does not match shape {shape}")
+        for c, n in zip(labels, shape):
+            if sizes.setdefault(c, n) != n:
+                raise ValueError(f"oracle einsum: axis {c!r} has sizes {sizes[c]} and {n}")
     r, swapped = cpu_plan(eq, a.shape, b.shape)
     if r["kind"] == "hadamard":
         out = np.empty(r["out_shape"], dtype=np.float32)
@@ -248,6 +259,22 @@ def bmm(A, B):
 
 def hadamard(a, b):
     a, b = _as_f32(a), _as_f32(b)
+    if a.shape != b.shape:
+        raise ValueError(f"hadamard: operand shapes {a.shape} and {b.shape} differ")
     out = np.empty(a.shape, dtype=np.float32)
     lib().oracle_hadamard_f32(a.ctypes.data, b.ctypes.data, out.ctypes.data, a.size)
     return out
+
+
+def linear_attention(q, k, v, m):
+    """The linear-attention chain as the reference runs it, three einsums with
+    float32 intermediates (tests/test_llm_ops.py:97-99 of the reference, with
+    the ``.to(dtype)`` casts read as float32):
+
+        A = einsum("tn,sn->ts", q, k); A = einsum("ts,ts->ts", A, m);
+        out = einsum("ts,sp->tp", A, v)
+
+    float16 operands are up-cast to float32 first (exact)."""
+    a = einsum("tn,sn->ts", q, k)
+    a = einsum("ts,ts->ts", a, m)
+    return einsum("ts,sp->tp", a, v)

@@ -74,6 +74,10 @@ struct ReduceArgs {
     int64_t c_bs[PE_MAX_DIMS];
 };
 
+// Deterministic split reduction: c = sum over the nsplit partial slabs in
+// ascending order (nsplit = 0 writes +0 everywhere).  Defined in pe_gemm.hip.
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(ReduceArgs r);
+
 // Host-side launch entry for one (dtype, tile) family; defined per family
 // in pe_gemm_f32.hip / pe_gemm_f16.hip.
 // Slab depth (k per LDS stage) of each family, for the split-K granularity.

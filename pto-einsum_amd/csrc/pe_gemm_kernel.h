@@ -468,7 +468,4 @@ __global__ __launch_bounds__(kGemmThreads, 2) void gemm_kernel(GemmArgs g) {
     }
 }
 
-// Deterministic split-K reduction: C = sum over splits in ascending order.
-__global__ __launch_bounds__(256) void splitk_reduce_kernel(ReduceArgs r);
-
 }  // namespace pe

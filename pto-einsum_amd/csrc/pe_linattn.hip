@@ -1,0 +1,429 @@
+// Fused linear-attention chain on CDNA4 matrix cores (gfx950):
+//
+//   out[t,p] = sum_s ((sum_n q[t,n] * k[s,n]) * m[t,s]) * v[s,p]
+//
+// The reference evaluates this as three einsums with float32 intermediates
+// (tests/test_llm_ops.py:81-107, benchmarks/complex/bench_linear_attention.py:62-94):
+//   A = einsum("tn,sn->ts", q, k); A = einsum("ts,ts->ts", A, m);
+//   out = einsum("ts,sp->tp", A, v)
+// which writes and re-reads two T x S float32 intermediates.  Here one launch
+// keeps each 32x32 block of A in registers:
+//
+//   1. S^T block = K_blk . Q_blk^T on MFMA (v_mfma_f32_32x32x16_f16 for float16
+//      q/k, v_mfma_f32_32x32x2_f32 for float32), float32 accumulation in two
+//      chains (even / odd k steps) added at the end.  With K as the A operand,
+//      lane l ends up holding row t = l%32 of the block and the 16 values
+//      s = 8*(r/4) + 4*(l/32) + r%4, r = 0..15.
+//   2. Those 16 values are multiplied by the mask in registers (one float32
+//      rounding, as the Hadamard step).
+//   3. They are exactly the A-operand registers of sixteen float32 MFMAs
+//      (v_mfma_f32_32x32x2_f32) whose k order is permuted to match: MFMA j
+//      pairs lane half h with s = 8*(j/4) + 4*h + j%4.  V is staged
+//      transposed in LDS so each lane reads its four consecutive s of one
+//      column p with one 16-byte read.
+//
+// Blocks of 32 t x 32 s whose mask is zero everywhere are skipped: their
+// contribution is exactly +-0 for finite operands.  The s axis is split over
+// blocks for parallelism; partial outputs are summed in split order by the
+// GEMM's deterministic reduction, so results are run-to-run identical.
+//
+// Loads are branch-free (clamped in-bounds address, then a select of zero):
+// a load on one side of a data-dependent branch makes the compiler wait for
+// it where the branches join, which serialises the prefetch.  For that the
+// kernel takes q / k rows as whole 16-byte vectors and mask rows as whole
+// 4-element vectors; operands whose rows are not laid out that way (base or
+// stride misaligned, N or S not a multiple of the vector) are first copied
+// into a zero-padded workspace by pad_rows_kernel.
+#include "pe_gemm_kernel.h"
+
+#include <algorithm>
+
+namespace pe {
+namespace {
+
+constexpr int kTB = 128;       // t rows per block (four waves x 32)
+constexpr int kPB = 128;       // p columns per block (four 32-column MFMA blocks)
+constexpr int kSB = 32;        // s per step
+constexpr int kVLD = kSB + 4;  // LDS pitch of the transposed V tile (conflict-free 16-byte reads)
+
+struct LinAttnArgs {
+    const void* q;
+    const void* k;
+    const void* v;
+    const void* m;
+    float* out;                // final [T][P], or split partials [split][T][P]
+    int32_t T, S, P;
+    int32_t NP;                // readable q / k row length: whole 16-byte vectors, zero past N
+    int32_t SP;                // readable mask row length: whole 4-vectors, zero past S
+    int64_t q_ts, k_ss, v_ss, m_ts;
+    int32_t s_per_split;       // multiple of kSB
+};
+
+// Q / K fragment of one MFMA k step: a 16-byte vector (float16) or one float.
+template <typename QK>
+struct Frag;
+
+template <>
+struct Frag<F16> {
+    using type = f16x8;
+    static constexpr int KSTEP = 16;
+    __device__ __forceinline__ static f32x16 mfma(type a, type b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+    }
+};
+
+template <>
+struct Frag<F32> {
+    using type = float;
+    static constexpr int KSTEP = 2;
+    __device__ __forceinline__ static f32x16 mfma(type a, type b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+    }
+};
+
+template <typename V>
+__device__ __forceinline__ V zero_unless(bool keep, V x) {
+    return keep ? x : V{};
+}
+
+// K tile of one s step in LDS: kSB rows of COLS elements at a padded pitch
+// that keeps the fragment reads conflict-free and 16-byte rows aligned.
+// Loaded cooperatively in 16-byte chunks.
+template <typename QK, int NSTEPS>
+struct KTile {
+    static constexpr int COLS = NSTEPS * Frag<QK>::KSTEP;
+    static constexpr int PITCH = COLS + (QK::kBytes == 2 ? 8 : 4);
+    static constexpr int VEC = 16 / QK::kBytes;
+    static constexpr int CPR = COLS / VEC;                 // chunks per row
+    static constexpr int PER_THREAD = kSB * CPR / 256;
+    static_assert(kSB * CPR % 256 == 0, "chunks split evenly over the block");
+};
+
+// NSTEPS: MFMA k steps covering N (N <= NSTEPS * KSTEP); VE / ME: element
+// types of v and m.
+//
+// Per s step (32 s), software-pipelined one step ahead: the V tile (32 x 128,
+// staged transposed), the K tile and this lane's mask values of step i+1 are
+// loaded into registers (raw element type, converted when committed) while
+// step i computes from LDS; two LDS stages mean one barrier per step.
+template <typename QK, int NSTEPS, typename VE, typename ME>
+__global__ __launch_bounds__(256, 2) void linattn_kernel(LinAttnArgs a) {
+    using T = typename QK::T;
+    using VT = typename VE::T;
+    using MT = typename ME::T;
+    using F = Frag<QK>;
+    using KT = KTile<QK, NSTEPS>;
+    using KChunk = typename Pack<KT::VEC, T>::type;
+    using MV = typename Pack<4, MT>::type;
+    __shared__ __attribute__((aligned(16))) float vt[2][kPB][kVLD];          // V tile, transposed: [p][s]
+    __shared__ __attribute__((aligned(16))) T kt[2][kSB * KT::PITCH];       // K tile: [s][n]
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int h = lane >> 5, l32 = lane & 31;
+    const int t0 = blockIdx.x * kTB + wave * 32;
+    const int p0 = blockIdx.y * kPB;
+    const int s_begin = blockIdx.z * a.s_per_split;
+    const int s_end = min(a.S, s_begin + a.s_per_split);
+    const int noff = QK::kBytes == 2 ? 8 * h : h;  // this lane's n offset inside a k step
+
+    // Q fragments of this lane's row t (B operand), held for the whole block.
+    const int trow = min(t0 + l32, a.T - 1);
+    const T* qrow = static_cast<const T*>(a.q) + int64_t(trow) * a.q_ts;
+    typename F::type qf[NSTEPS];
+#pragma unroll
+    for (int kk = 0; kk < NSTEPS; ++kk) {
+        const int n = kk * F::KSTEP + noff;
+        const bool ok = n < a.NP;
+        qf[kk] = zero_unless(ok, *reinterpret_cast<const typename F::type*>(qrow + (ok ? n : 0)));
+    }
+
+    f32x16 acc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[j][r] = 0.0f;
+
+    // Registers of the step in flight.
+    const int vp = tid & 127, vs0 = (tid >> 7) * 16;  // this thread's V column and 16 s rows
+    VT vpre[16];
+    KChunk kpre[KT::PER_THREAD];
+    MV mpre[4];
+    const MT* mrow = static_cast<const MT*>(a.m) + int64_t(trow) * a.m_ts;
+    const VT* vcol = static_cast<const VT*>(a.v) + min(p0 + vp, a.P - 1);
+    const bool vp_ok = p0 + vp < a.P;
+
+    auto prefetch = [&](int sb) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int s = sb + vs0 + i;
+            vpre[i] = zero_unless(vp_ok && s < a.S, vcol[int64_t(min(s, a.S - 1)) * a.v_ss]);
+        }
+#pragma unroll
+        for (int i = 0; i < KT::PER_THREAD; ++i) {
+            const int c = tid + 256 * i;
+            const int s = sb + c / KT::CPR, col = (c % KT::CPR) * KT::VEC;
+            const bool ok = s < a.S && col < a.NP;
+            const T* src = static_cast<const T*>(a.k) + int64_t(min(s, a.S - 1)) * a.k_ss + (col < a.NP ? col : 0);
+            kpre[i] = zero_unless(ok, *reinterpret_cast<const KChunk*>(src));
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int s = sb + 8 * q + 4 * h;
+            const bool ok = s < a.SP;
+            mpre[q] = zero_unless(ok, *reinterpret_cast<const MV*>(mrow + (ok ? s : 0)));
+        }
+    };
+
+    if (s_begin < s_end) prefetch(s_begin);
+    int stage = 0;
+    for (int sb = s_begin; sb < s_end; sb += kSB, stage ^= 1) {
+        // Commit the prefetched step to this stage (its readers from two steps
+        // ago passed the previous barrier after finishing).
+#pragma unroll
+        for (int i = 0; i < 16; i += 4) {
+            f32x4 w = {float(vpre[i]), float(vpre[i + 1]), float(vpre[i + 2]), float(vpre[i + 3])};
+            *reinterpret_cast<f32x4*>(&vt[stage][vp][vs0 + i]) = w;
+        }
+#pragma unroll
+        for (int i = 0; i < KT::PER_THREAD; ++i) {
+            const int c = tid + 256 * i;
+            *reinterpret_cast<KChunk*>(&kt[stage][(c / KT::CPR) * KT::PITCH + (c % KT::CPR) * KT::VEC]) = kpre[i];
+        }
+        float mv[16];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) mv[4 * q + i] = float(mpre[q][i]);
+        __syncthreads();
+        if (sb + kSB < s_end) prefetch(sb + kSB);
+
+        bool nz = false;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) nz = nz || (mv[r] != 0.0f);
+        if (__any(nz)) {
+            // 1. S^T block: rows s (this lane: 16 of them), column t = l32, in
+            //    two accumulation chains (even / odd k steps).
+            const T* krow = &kt[stage][l32 * KT::PITCH + noff];
+            f32x16 sacc[2];
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) sacc[c][r] = 0.0f;
+#pragma unroll
+            for (int kk = 0; kk < NSTEPS; ++kk) {
+                const typename F::type kf = *reinterpret_cast<const typename F::type*>(krow + kk * F::KSTEP);
+                sacc[kk & 1] = F::mfma(kf, qf[kk], sacc[kk & 1]);
+            }
+            // 2. Mask product (float32, one rounding).
+            float av[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) av[r] = (sacc[0][r] + sacc[1][r]) * mv[r];
+            // 3. out[t, p] += sum_s A[t, s] v[s, p]; MFMA j takes s = 8*(j/4) + 4*h + j%4.
+            //    The four 32-column blocks are interleaved: four independent chains.
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                f32x4 vf[4];
+#pragma unroll
+                for (int jb = 0; jb < 4; ++jb)
+                    vf[jb] = *reinterpret_cast<const f32x4*>(&vt[stage][32 * jb + l32][8 * q + 4 * h]);
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int jb = 0; jb < 4; ++jb)
+                        acc[jb] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[4 * q + i], vf[jb][i], acc[jb], 0, 0, 0);
+            }
+        }
+    }
+
+    // Store: lane l, register r holds out[t0 + 8*(r/4) + 4*h + r%4][p0 + 32*jb + l32].
+    float* out = a.out + int64_t(blockIdx.z) * a.T * a.P;
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb) {
+        const int p = p0 + 32 * jb + l32;
+        if (p >= a.P) continue;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int t = t0 + 8 * (r >> 2) + 4 * h + (r & 3);
+            if (t < a.T) out[int64_t(t) * a.P + p] = acc[jb][r];
+        }
+    }
+}
+
+// dst[r][c] = c < cols ? src[r * src_stride + c] : 0, for c < pitch.
+template <typename W>
+__global__ __launch_bounds__(256) void pad_rows_kernel(const W* __restrict__ src, int64_t src_stride, W* __restrict__ dst,
+                                                       int64_t rows, int64_t cols, int64_t pitch) {
+    const int64_t n = rows * pitch;
+    for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += int64_t(gridDim.x) * 256) {
+        const int64_t r = i / pitch, c = i - r * pitch;
+        dst[i] = c < cols ? src[r * src_stride + c] : W(0);
+    }
+}
+
+int64_t round_up(int64_t x, int64_t m) { return ceil_div(x, m) * m; }
+
+// Workspace: split partials, then zero-padded copies of the operands whose
+// rows the kernel cannot read as whole vectors.
+struct Plan {
+    int nsplit;
+    int s_per_split;
+    bool stage_q, stage_k, stage_m;
+    int64_t NP, SP;
+    int64_t q_off, k_off, m_off;
+    int64_t ws_bytes;
+};
+
+Plan plan(const pe_linattn_desc& d, const void* q, const void* k, const void* m) {
+    Plan p{};
+    const int64_t blocks_tp = ceil_div(d.T, kTB) * ceil_div(d.P, kPB);
+    const int64_t sblocks = std::max<int64_t>(1, ceil_div(d.S, kSB));
+    int64_t split = d.split > 0 ? d.split : ceil_div(2 * int64_t(cu_count()), blocks_tp);
+    split = std::max<int64_t>(1, std::min(split, sblocks));
+    p.s_per_split = int(ceil_div(sblocks, split) * kSB);
+    p.nsplit = int(ceil_div(std::max<int64_t>(d.S, 1), p.s_per_split));
+    const int qb = d.qk_dtype == PE_F16 ? 2 : 4, mb = d.m_dtype == PE_F16 ? 2 : 4;
+    const int qvec = 16 / qb;
+    p.NP = round_up(d.N, qvec);
+    p.SP = round_up(d.S, 4);
+    // A null pointer (the size query) is taken as aligned: the workspace size
+    // covers operands whose base addresses are 16-byte aligned.
+    p.stage_q = (q && !aligned(q, 16)) || d.q_ts % qvec != 0 || d.N % qvec != 0;
+    p.stage_k = (k && !aligned(k, 16)) || d.k_ss % qvec != 0 || d.N % qvec != 0;
+    p.stage_m = (m && !aligned(m, 4 * mb)) || d.m_ts % 4 != 0 || d.S % 4 != 0;
+    int64_t off = p.nsplit > 1 ? round_up(int64_t(p.nsplit) * d.T * d.P * 4, 256) : 0;
+    p.q_off = off; if (p.stage_q) off += round_up(d.T * p.NP * qb, 256);
+    p.k_off = off; if (p.stage_k) off += round_up(d.S * p.NP * qb, 256);
+    p.m_off = off; if (p.stage_m) off += round_up(d.T * p.SP * mb, 256);
+    p.ws_bytes = off;
+    return p;
+}
+
+int validate(const pe_linattn_desc& d) {
+    auto dt_ok = [](int x) { return x == PE_F32 || x == PE_F16; };
+    if (!dt_ok(d.qk_dtype) || !dt_ok(d.v_dtype) || !dt_ok(d.m_dtype))
+        return fail(PE_ERR_UNSUPPORTED, "linear_attention: dtypes must be PE_F32 or PE_F16");
+    if (d.T < 0 || d.S < 0 || d.N < 0 || d.P < 0) return fail(PE_ERR_INVALID, "linear_attention: negative extent");
+    if (d.split < 0) return fail(PE_ERR_INVALID, "linear_attention: split must be >= 0");
+    const int64_t nmax = d.qk_dtype == PE_F16 ? 256 : 128;
+    if (d.N > nmax) return fail(PE_ERR_UNSUPPORTED, "linear_attention: N above " + std::to_string(nmax));
+    if (d.T >= (int64_t(1) << 31) || d.S >= (int64_t(1) << 31) || d.P >= (int64_t(1) << 31) ||
+        d.T * d.P >= (int64_t(1) << 32))
+        return fail(PE_ERR_UNSUPPORTED, "linear_attention: extents too large");
+    if (d.q_ts < 0 || d.k_ss < 0 || d.v_ss < 0 || d.m_ts < 0)
+        return fail(PE_ERR_INVALID, "linear_attention: negative stride");
+    if (d.T == 0 || d.P == 0 || d.S == 0 || d.N == 0) return PE_OK;
+    if ((d.T - 1) * d.q_ts + d.N > d.q_numel) return fail(PE_ERR_BOUNDS, "linear_attention: q strides address past its extent");
+    if ((d.S - 1) * d.k_ss + d.N > d.k_numel) return fail(PE_ERR_BOUNDS, "linear_attention: k strides address past its extent");
+    if ((d.S - 1) * d.v_ss + d.P > d.v_numel) return fail(PE_ERR_BOUNDS, "linear_attention: v strides address past its extent");
+    if ((d.T - 1) * d.m_ts + d.S > d.m_numel) return fail(PE_ERR_BOUNDS, "linear_attention: m strides address past its extent");
+    return PE_OK;
+}
+
+template <typename QK, int NSTEPS, typename VE, typename ME>
+hipError_t launch(const LinAttnArgs& a, dim3 grid, hipStream_t s) {
+    hipLaunchKernelGGL((linattn_kernel<QK, NSTEPS, VE, ME>), grid, dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+template <typename QK, int NSTEPS>
+hipError_t launch_vm(const LinAttnArgs& a, int vdt, int mdt, dim3 grid, hipStream_t s) {
+    if (vdt == PE_F16) return mdt == PE_F16 ? launch<QK, NSTEPS, F16, F16>(a, grid, s) : launch<QK, NSTEPS, F16, F32>(a, grid, s);
+    return mdt == PE_F16 ? launch<QK, NSTEPS, F32, F16>(a, grid, s) : launch<QK, NSTEPS, F32, F32>(a, grid, s);
+}
+
+hipError_t pad_rows(const void* src, int64_t stride, void* dst, int64_t rows, int64_t cols, int64_t pitch,
+                    int elem_bytes, hipStream_t s) {
+    const int grid = int(std::max<int64_t>(1, std::min<int64_t>(ceil_div(rows * pitch, 256), cu_count() * 16)));
+    if (elem_bytes == 2)
+        hipLaunchKernelGGL(pad_rows_kernel<uint16_t>, dim3(grid), dim3(256), 0, s, static_cast<const uint16_t*>(src),
+                           stride, static_cast<uint16_t*>(dst), rows, cols, pitch);
+    else
+        hipLaunchKernelGGL(pad_rows_kernel<uint32_t>, dim3(grid), dim3(256), 0, s, static_cast<const uint32_t*>(src),
+                           stride, static_cast<uint32_t*>(dst), rows, cols, pitch);
+    return hipGetLastError();
+}
+
+}  // namespace
+}  // namespace pe
+
+extern "C" int64_t pe_linear_attention_workspace_bytes(const pe_linattn_desc* d) {
+    if (!d || pe::validate(*d) != PE_OK) return 0;
+    return pe::plan(*d, nullptr, nullptr, nullptr).ws_bytes;
+}
+
+extern "C" int pe_linear_attention(const pe_linattn_desc* d, const void* q, const void* k, const void* v,
+                                   const void* m, float* out, void* ws, int64_t ws_bytes, void* stream) {
+    using namespace pe;
+    if (!d) return fail(PE_ERR_INVALID, "linear_attention: null descriptor");
+    int st = validate(*d);
+    if (st != PE_OK) return st;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (d->T == 0 || d->P == 0) return PE_OK;
+
+    ReduceArgs r{};
+    r.c = out;
+    r.per_split = uint32_t(d->T * d->P);
+    r.n_div.init(uint32_t(d->P));
+    r.m_div.init(uint32_t(d->T));
+    r.c_ms = d->P;
+    r.c_ns = 1;
+    r.nbatch = 0;
+    r.store_nt = 0;
+    const int rgrid = int(std::max<int64_t>(1, std::min<int64_t>(ceil_div(r.per_split, 256), cu_count() * 8)));
+    if (d->S == 0 || d->N == 0) {
+        // Empty sums: every A[t, s] is +0 (N = 0) or there is no s at all,
+        // so every output is +0 (operands are not read).
+        r.nsplit = 0;
+        r.partial = nullptr;
+        hipLaunchKernelGGL(splitk_reduce_kernel, dim3(rgrid), dim3(256), 0, s, r);
+        PE_CHECK_HIP(hipGetLastError());
+        return PE_OK;
+    }
+    const Plan pl = plan(*d, q, k, m);
+    if (pl.ws_bytes > 0 && (!ws || ws_bytes < pl.ws_bytes))
+        return fail(PE_ERR_WORKSPACE, "linear_attention: workspace missing or too small (" +
+                                          std::to_string(pl.ws_bytes) + " bytes needed; operands not "
+                                          "16-byte aligned need more than the size query reports)");
+
+    LinAttnArgs a{};
+    char* wsb = static_cast<char*>(ws);
+    const int qb = d->qk_dtype == PE_F16 ? 2 : 4, mb = d->m_dtype == PE_F16 ? 2 : 4;
+    a.q = q; a.k = k; a.v = v; a.m = m;
+    a.q_ts = d->q_ts; a.k_ss = d->k_ss; a.v_ss = d->v_ss; a.m_ts = d->m_ts;
+    if (pl.stage_q) {
+        PE_CHECK_HIP(pad_rows(q, d->q_ts, wsb + pl.q_off, d->T, d->N, pl.NP, qb, s));
+        a.q = wsb + pl.q_off;
+        a.q_ts = pl.NP;
+    }
+    if (pl.stage_k) {
+        PE_CHECK_HIP(pad_rows(k, d->k_ss, wsb + pl.k_off, d->S, d->N, pl.NP, qb, s));
+        a.k = wsb + pl.k_off;
+        a.k_ss = pl.NP;
+    }
+    if (pl.stage_m) {
+        PE_CHECK_HIP(pad_rows(m, d->m_ts, wsb + pl.m_off, d->T, d->S, pl.SP, mb, s));
+        a.m = wsb + pl.m_off;
+        a.m_ts = pl.SP;
+    }
+    a.out = pl.nsplit > 1 ? reinterpret_cast<float*>(wsb) : out;
+    a.T = int32_t(d->T); a.S = int32_t(d->S); a.P = int32_t(d->P);
+    a.NP = int32_t(pl.NP);
+    a.SP = int32_t(pl.SP);
+    a.s_per_split = pl.s_per_split;
+    const dim3 grid(uint32_t(ceil_div(d->T, kTB)), uint32_t(ceil_div(d->P, kPB)), uint32_t(pl.nsplit));
+    hipError_t e;
+    if (d->qk_dtype == PE_F16)
+        e = d->N <= 128 ? launch_vm<F16, 8>(a, d->v_dtype, d->m_dtype, grid, s)
+                        : launch_vm<F16, 16>(a, d->v_dtype, d->m_dtype, grid, s);
+    else
+        e = launch_vm<F32, 64>(a, d->v_dtype, d->m_dtype, grid, s);
+    PE_CHECK_HIP(e);
+    if (pl.nsplit > 1) {
+        r.nsplit = pl.nsplit;
+        r.partial = reinterpret_cast<const float*>(wsb);
+        hipLaunchKernelGGL(splitk_reduce_kernel, dim3(rgrid), dim3(256), 0, s, r);
+        PE_CHECK_HIP(hipGetLastError());
+    }
+    return PE_OK;
+}

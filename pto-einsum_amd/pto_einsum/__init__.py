@@ -6,12 +6,17 @@ Public API, unchanged from the reference (src/pto_einsum/__init__.py:12-15):
     EinsumBuilder(equation, shapes, dtype)  -> reusable compiled runner
     INCLUDE_DIR                             -> headers the JIT sources compile against
 
+Beyond the reference's surface:
+
+    linear_attention(q, k, v, m)            -> fused einsum("tn,sn,sp,ts->tp"), float32
+
 Example:
     >>> from pto_einsum import einsum
     >>> c = einsum("ij, jk -> ik", a, b)    # a, b are tensors on the GPU
 """
 
 from .builder import EinsumBuilder, INCLUDE_DIR, einsum
+from .linattn import linear_attention
 
-__all__ = ["einsum", "EinsumBuilder", "INCLUDE_DIR"]
+__all__ = ["einsum", "EinsumBuilder", "INCLUDE_DIR", "linear_attention"]
 __version__ = "0.1.0"

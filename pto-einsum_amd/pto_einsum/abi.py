@@ -1,7 +1,8 @@
 """ctypes mirrors of the core library's C structs (include/pto_einsum_hip.h).
 
 Lets Python callers (and the component tests) drive the core launchers
-directly: ``pe_product``, ``pe_permute``, ``pe_gemm`` and the plan executor.
+directly: ``pe_product``, ``pe_permute``, ``pe_gemm``, ``pe_linear_attention``
+and the plan executor.
 """
 from __future__ import annotations
 
@@ -45,6 +46,16 @@ class EinsumPlan(ctypes.Structure):
                 ("ws0_off", ctypes.c_int64), ("ws1_off", ctypes.c_int64),
                 ("wsout_off", ctypes.c_int64), ("wsgemm_off", ctypes.c_int64),
                 ("ws_bytes", ctypes.c_int64)]
+
+
+class LinAttnDesc(ctypes.Structure):
+    _fields_ = [("qk_dtype", ctypes.c_int32), ("v_dtype", ctypes.c_int32), ("m_dtype", ctypes.c_int32),
+                ("split", ctypes.c_int32),
+                ("T", ctypes.c_int64), ("S", ctypes.c_int64), ("N", ctypes.c_int64), ("P", ctypes.c_int64),
+                ("q_ts", ctypes.c_int64), ("k_ss", ctypes.c_int64), ("v_ss", ctypes.c_int64),
+                ("m_ts", ctypes.c_int64),
+                ("q_numel", ctypes.c_int64), ("k_numel", ctypes.c_int64), ("v_numel", ctypes.c_int64),
+                ("m_numel", ctypes.c_int64)]
 
 
 def _set(arr, values: Sequence[int]):
@@ -96,6 +107,10 @@ def bind(lib=None):
     lib.pe_einsum_setup.restype = vp
     lib.pe_einsum_teardown.argtypes = [vp]
     lib.pe_einsum_run.argtypes = [ctypes.POINTER(EinsumPlan), vp, vp, vp, vp]
-    for f in ("pe_product", "pe_permute", "pe_gemm", "pe_einsum_exec", "pe_einsum_teardown", "pe_einsum_run"):
+    lib.pe_linear_attention.argtypes = [ctypes.POINTER(LinAttnDesc), vp, vp, vp, vp, vp, vp, ctypes.c_int64, vp]
+    lib.pe_linear_attention_workspace_bytes.argtypes = [ctypes.POINTER(LinAttnDesc)]
+    lib.pe_linear_attention_workspace_bytes.restype = ctypes.c_int64
+    for f in ("pe_product", "pe_permute", "pe_gemm", "pe_einsum_exec", "pe_einsum_teardown", "pe_einsum_run",
+              "pe_linear_attention"):
         getattr(lib, f).restype = ctypes.c_int
     return lib

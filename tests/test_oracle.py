@@ -244,3 +244,72 @@ def test_summation_order_is_pinned():
     rev = oracle.einsum("ij,jk->ik", a[:, ::-1].copy(), b)
     assert not np.array_equal(_bits(fwd), _bits(rev))
     assert np.array_equal(_bits(fwd), _bits(_brute("ij,jk->ik", a, b)))
+
+
+# ---- linear-attention chain (composition of pinned einsum steps) ----
+
+LINATTN_CASES = [(96, 96, 64, 128), (320, 320, 64, 128)]
+
+
+def _linattn_inputs(T, S, N, P, seed=0):
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((T, N)).astype(np.float32)
+    k = rng.standard_normal((S, N)).astype(np.float32)
+    v = rng.standard_normal((S, P)).astype(np.float32)
+    m = np.tril(rng.random((T, S))).astype(np.float32)   # not symmetric: a transposed mask is caught
+    return q, k, v, m
+
+
+@pytest.mark.parametrize("T,S,N,P", LINATTN_CASES)
+def test_oracle_linear_attention_matches_reference_steps(T, S, N, P):
+    """The composed chain equals the reference build run step by step (the
+    steps are the reference's own test shapes, tests/test_llm_ops.py:81-107)."""
+    q, k, v, m = _linattn_inputs(T, S, N, P, seed=3)
+    steps = [("tn,sn->ts", (T, N), (S, N)), ("ts,ts->ts", (T, S), (T, S)), ("ts,sp->tp", (T, S), (S, P))]
+    if not all(os.path.exists(ref_build.so_path(*st)) for st in steps):
+        pytest.skip("oracle/_ref not built (no /root/reference here)")
+    a = ref_build.run(steps[0][0], q, k)
+    a = ref_build.run(steps[1][0], a, m)
+    want = ref_build.run(steps[2][0], a, v)
+    assert np.array_equal(_bits(oracle.linear_attention(q, k, v, m)), _bits(want))
+
+
+@pytest.mark.parametrize("T,S,N,P", LINATTN_CASES + [(7, 5, 3, 4), (1, 9, 16, 2)])
+def test_oracle_linear_attention_close_to_float64(T, S, N, P):
+    q, k, v, m = _linattn_inputs(T, S, N, P, seed=4)
+    ref = torch.einsum("tn,sn,sp,ts->tp", *(torch.from_numpy(x).double() for x in (q, k, v, m))).numpy()
+    got = oracle.linear_attention(q, k, v, m)
+    assert np.abs(got - ref).max() <= 2e-5 * np.abs(ref).max()
+
+
+def _linattn_brute(q, k, v, m):
+    T, N = q.shape
+    S, P = v.shape
+    a = np.zeros((T, S), dtype=np.float32)
+    for t in range(T):
+        for s in range(S):
+            acc = np.float32(0.0)
+            for n in range(N):
+                acc = np.float32(acc + np.float32(q[t, n]) * np.float32(k[s, n]))
+            a[t, s] = np.float32(acc * m[t, s])
+    out = np.zeros((T, P), dtype=np.float32)
+    for t in range(T):
+        for p in range(P):
+            acc = np.float32(0.0)
+            for s in range(S):
+                acc = np.float32(acc + a[t, s] * np.float32(v[s, p]))
+            out[t, p] = acc
+    return out
+
+
+def test_oracle_linear_attention_brute_force():
+    q, k, v, m = _linattn_inputs(6, 7, 5, 3, seed=5)
+    assert np.array_equal(_bits(oracle.linear_attention(q, k, v, m)), _bits(_linattn_brute(q, k, v, m)))
+
+
+def test_linear_attention_checks_catch_a_transposed_mask():
+    """A chain that applied the mask transposed must fail the float64 pin."""
+    q, k, v, m = _linattn_inputs(12, 12, 8, 4, seed=6)
+    ref = torch.einsum("tn,sn,sp,ts->tp", *(torch.from_numpy(x).double() for x in (q, k, v, m))).numpy()
+    wrong = oracle.linear_attention(q, k, v, np.ascontiguousarray(m.T))
+    assert np.abs(wrong - ref).max() > 2e-5 * np.abs(ref).max()
