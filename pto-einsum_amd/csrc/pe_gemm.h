@@ -75,8 +75,9 @@ struct ReduceArgs {
 };
 
 // Deterministic split reduction: c = sum over the nsplit partial slabs in
-// ascending order (nsplit = 0 writes +0 everywhere).  Defined in pe_gemm.hip.
-__global__ __launch_bounds__(256) void splitk_reduce_kernel(ReduceArgs r);
+// ascending order from +0 (nsplit = 0 writes +0 everywhere).  Enqueues the
+// reduction kernel (pe_gemm.hip).
+hipError_t launch_splitk_reduce(const ReduceArgs& r, hipStream_t s);
 
 // Host-side launch entry for one (dtype, tile) family; defined per family
 // in pe_gemm_f32.hip / pe_gemm_f16.hip.

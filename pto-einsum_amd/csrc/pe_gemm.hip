@@ -1,7 +1,7 @@
 // Host side of the batched MFMA GEMM: descriptor validation, operand layout
 // classification, tile / split-K choice and the deterministic split-K
 // reduction kernel.
-#include "pe_gemm.h"
+#include "pe_gemm_kernel.h"
 
 #include <algorithm>
 
@@ -26,23 +26,65 @@
 
 namespace pe {
 
+// Deterministic split reduction.  Each thread owns VEC consecutive outputs
+// and sums their nsplit partials in ascending split order, from +0, exactly
+// as a sequential loop would; the partial loads are issued eight splits at a
+// time so their latencies overlap instead of adding up.
+template <int VEC>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(ReduceArgs r) {
+    using V = typename Pack<VEC, float>::type;
+    const uint32_t nv = r.per_split / VEC;
     const uint32_t stride = gridDim.x * 256;
-    for (uint32_t idx = blockIdx.x * 256 + threadIdx.x; idx < r.per_split; idx += stride) {
-        float acc = 0.0f;
-        for (int s = 0; s < r.nsplit; ++s) acc = acc + r.partial[int64_t(s) * r.per_split + idx];
-        uint32_t rest, n, batch, m;
-        r.n_div.divmod(idx, rest, n);
-        r.m_div.divmod(rest, batch, m);
-        int64_t off = int64_t(m) * r.c_ms + int64_t(n) * r.c_ns;
-        for (int d = r.nbatch - 1; d >= 0; --d) {
-            uint32_t q, rr;
-            r.batch_div[d].divmod(batch, q, rr);
-            off += int64_t(rr) * r.c_bs[d];
-            batch = q;
+    for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < nv; i += stride) {
+        float acc[VEC];
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) acc[e] = 0.0f;
+        for (int s0 = 0; s0 < r.nsplit; s0 += 8) {
+            V x[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int sp = min(s0 + u, r.nsplit - 1);
+                x[u] = *reinterpret_cast<const V*>(r.partial + int64_t(sp) * r.per_split + int64_t(i) * VEC);
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                if (s0 + u < r.nsplit) {
+                    if constexpr (VEC == 1) {
+                        acc[0] = acc[0] + x[u];
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < VEC; ++e) acc[e] = acc[e] + x[u][e];
+                    }
+                }
+            }
         }
-        store_f(r.c + off, acc, r.store_nt != 0);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+            const uint32_t idx = i * VEC + e;
+            uint32_t rest, n, batch, m;
+            r.n_div.divmod(idx, rest, n);
+            r.m_div.divmod(rest, batch, m);
+            int64_t off = int64_t(m) * r.c_ms + int64_t(n) * r.c_ns;
+            for (int d = r.nbatch - 1; d >= 0; --d) {
+                uint32_t q, rr;
+                r.batch_div[d].divmod(batch, q, rr);
+                off += int64_t(rr) * r.c_bs[d];
+                batch = q;
+            }
+            store_f(r.c + off, acc[e], r.store_nt != 0);
+        }
     }
+}
+
+hipError_t launch_splitk_reduce(const ReduceArgs& r, hipStream_t s) {
+    const bool vec = r.per_split % 4 == 0 && (r.nsplit == 0 || aligned(r.partial, 16));
+    const int64_t items = vec ? r.per_split / 4 : r.per_split;
+    const int grid = int(std::max<int64_t>(1, std::min<int64_t>(ceil_div(items, 256), cu_count() * 8)));
+    if (vec)
+        hipLaunchKernelGGL(splitk_reduce_kernel<4>, dim3(grid), dim3(256), 0, s, r);
+    else
+        hipLaunchKernelGGL(splitk_reduce_kernel<1>, dim3(grid), dim3(256), 0, s, r);
+    return hipGetLastError();
 }
 
 namespace {
@@ -204,15 +246,11 @@ extern "C" int pe_gemm(const pe_gemm_desc* d, const void* a, const void* b, floa
         r.batch_div[i].init(uint32_t(d->batch_shape[i]));
         r.c_bs[i] = d->c_bstride[i];
     }
-    auto reduce_grid = [&]() {
-        return int(std::max<int64_t>(1, std::min<int64_t>(ceil_div(r.per_split, 256), cu_count() * 8)));
-    };
     if (d->K == 0) {  // empty contraction: every output is the empty sum, +0
         if (nb * d->M * d->N >= (int64_t(1) << 32)) return fail(PE_ERR_UNSUPPORTED, "gemm: output too large");
         r.nsplit = 0;
         r.partial = nullptr;
-        hipLaunchKernelGGL(splitk_reduce_kernel, dim3(reduce_grid()), dim3(256), 0, s, r);
-        PE_CHECK_HIP(hipGetLastError());
+        PE_CHECK_HIP(launch_splitk_reduce(r, s));
         return PE_OK;
     }
 
@@ -255,8 +293,7 @@ extern "C" int pe_gemm(const pe_gemm_desc* d, const void* a, const void* b, floa
         r.nsplit = ch.nsplit;
         r.partial = static_cast<const float*>(ws);
         r.store_nt = nb * d->M * d->N * 4 >= PE_NT_MIN_BYTES;
-        hipLaunchKernelGGL(splitk_reduce_kernel, dim3(reduce_grid()), dim3(256), 0, s, r);
-        PE_CHECK_HIP(hipGetLastError());
+        PE_CHECK_HIP(launch_splitk_reduce(r, s));
     }
     return PE_OK;
 }

@@ -144,34 +144,55 @@ __global__ __launch_bounds__(256, 2) void linattn_kernel(LinAttnArgs a) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[j][r] = 0.0f;
 
-    // Registers of the step in flight.
+    // Registers of the step in flight, and this thread's fixed load addresses.
     const int vp = tid & 127, vs0 = (tid >> 7) * 16;  // this thread's V column and 16 s rows
     VT vpre[16];
     KChunk kpre[KT::PER_THREAD];
     MV mpre[4];
-    const MT* mrow = static_cast<const MT*>(a.m) + int64_t(trow) * a.m_ts;
-    const VT* vcol = static_cast<const VT*>(a.v) + min(p0 + vp, a.P - 1);
-    const bool vp_ok = p0 + vp < a.P;
+    const VT* vrow0 = static_cast<const VT*>(a.v) + int64_t(vs0) * a.v_ss + min(p0 + vp, a.P - 1);
+    const T* krow0[KT::PER_THREAD];
+    bool kcol_ok[KT::PER_THREAD];
+#pragma unroll
+    for (int i = 0; i < KT::PER_THREAD; ++i) {
+        const int c = tid + 256 * i, col = (c % KT::CPR) * KT::VEC;
+        kcol_ok[i] = col < a.NP;
+        krow0[i] = static_cast<const T*>(a.k) + int64_t(c / KT::CPR) * a.k_ss + (kcol_ok[i] ? col : 0);
+    }
+    const MT* mrow4 = static_cast<const MT*>(a.m) + int64_t(trow) * a.m_ts + 4 * h;
+    const bool k_all_cols = a.NP >= KT::COLS;  // no K chunk lies past N
 
+    // Raw loads only: the zero selects happen when the step is committed, one
+    // step later, so nothing waits on the loads here.  A step whose 32 s all
+    // lie inside S needs no clamping (the usual case); V columns past P feed
+    // only outputs that are never stored, so they are not masked at all.
     auto prefetch = [&](int sb) {
+        if (sb + kSB <= a.S) {
+            const VT* vp_ = vrow0 + int64_t(sb) * a.v_ss;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int s = sb + vs0 + i;
-            vpre[i] = zero_unless(vp_ok && s < a.S, vcol[int64_t(min(s, a.S - 1)) * a.v_ss]);
-        }
+            for (int i = 0; i < 16; ++i) {
+                vpre[i] = *vp_;
+                vp_ += a.v_ss;
+            }
 #pragma unroll
-        for (int i = 0; i < KT::PER_THREAD; ++i) {
-            const int c = tid + 256 * i;
-            const int s = sb + c / KT::CPR, col = (c % KT::CPR) * KT::VEC;
-            const bool ok = s < a.S && col < a.NP;
-            const T* src = static_cast<const T*>(a.k) + int64_t(min(s, a.S - 1)) * a.k_ss + (col < a.NP ? col : 0);
-            kpre[i] = zero_unless(ok, *reinterpret_cast<const KChunk*>(src));
-        }
+            for (int i = 0; i < KT::PER_THREAD; ++i)
+                kpre[i] = *reinterpret_cast<const KChunk*>(krow0[i] + int64_t(sb) * a.k_ss);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int s = sb + 8 * q + 4 * h;
-            const bool ok = s < a.SP;
-            mpre[q] = zero_unless(ok, *reinterpret_cast<const MV*>(mrow + (ok ? s : 0)));
+            for (int q = 0; q < 4; ++q) mpre[q] = *reinterpret_cast<const MV*>(mrow4 + sb + 8 * q);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+                vpre[i] = vrow0[int64_t(min(sb + vs0 + i, a.S - 1) - vs0) * a.v_ss];
+#pragma unroll
+            for (int i = 0; i < KT::PER_THREAD; ++i) {
+                const int s = sb + (tid + 256 * i) / KT::CPR;
+                kpre[i] = *reinterpret_cast<const KChunk*>(krow0[i] +
+                                                           int64_t(min(s, a.S - 1) - (s - sb)) * a.k_ss);
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int s = sb + 8 * q + 4 * h;
+                mpre[q] = *reinterpret_cast<const MV*>(mrow4 - 4 * h + (s < a.SP ? s : 0));
+            }
         }
     };
 
@@ -179,22 +200,48 @@ __global__ __launch_bounds__(256, 2) void linattn_kernel(LinAttnArgs a) {
     int stage = 0;
     for (int sb = s_begin; sb < s_end; sb += kSB, stage ^= 1) {
         // Commit the prefetched step to this stage (its readers from two steps
-        // ago passed the previous barrier after finishing).
-#pragma unroll
-        for (int i = 0; i < 16; i += 4) {
-            f32x4 w = {float(vpre[i]), float(vpre[i + 1]), float(vpre[i + 2]), float(vpre[i + 3])};
-            *reinterpret_cast<f32x4*>(&vt[stage][vp][vs0 + i]) = w;
-        }
-#pragma unroll
-        for (int i = 0; i < KT::PER_THREAD; ++i) {
-            const int c = tid + 256 * i;
-            *reinterpret_cast<KChunk*>(&kt[stage][(c / KT::CPR) * KT::PITCH + (c % KT::CPR) * KT::VEC]) = kpre[i];
-        }
+        // ago passed the previous barrier after finishing), zeroing what lies
+        // past S or N.
+        const bool full = sb + kSB <= a.S;
         float mv[16];
+        if (full) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
+            for (int i = 0; i < 16; i += 4) {
+                f32x4 w = {float(vpre[i]), float(vpre[i + 1]), float(vpre[i + 2]), float(vpre[i + 3])};
+                *reinterpret_cast<f32x4*>(&vt[stage][vp][vs0 + i]) = w;
+            }
 #pragma unroll
-            for (int i = 0; i < 4; ++i) mv[4 * q + i] = float(mpre[q][i]);
+            for (int i = 0; i < KT::PER_THREAD; ++i) {
+                const int c = tid + 256 * i;
+                *reinterpret_cast<KChunk*>(&kt[stage][(c / KT::CPR) * KT::PITCH + (c % KT::CPR) * KT::VEC]) =
+                    k_all_cols ? kpre[i] : zero_unless(kcol_ok[i], kpre[i]);
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) mv[4 * q + i] = float(mpre[q][i]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; i += 4) {
+                f32x4 w;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) w[j] = sb + vs0 + i + j < a.S ? float(vpre[i + j]) : 0.0f;
+                *reinterpret_cast<f32x4*>(&vt[stage][vp][vs0 + i]) = w;
+            }
+#pragma unroll
+            for (int i = 0; i < KT::PER_THREAD; ++i) {
+                const int c = tid + 256 * i;
+                const bool ok = sb + c / KT::CPR < a.S && kcol_ok[i];
+                *reinterpret_cast<KChunk*>(&kt[stage][(c / KT::CPR) * KT::PITCH + (c % KT::CPR) * KT::VEC]) =
+                    zero_unless(ok, kpre[i]);
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const bool ok = sb + 8 * q + 4 * h < a.SP;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) mv[4 * q + i] = ok ? float(mpre[q][i]) : 0.0f;
+            }
+        }
         __syncthreads();
         if (sb + kSB < s_end) prefetch(sb + kSB);
 
@@ -370,14 +417,12 @@ extern "C" int pe_linear_attention(const pe_linattn_desc* d, const void* q, cons
     r.c_ns = 1;
     r.nbatch = 0;
     r.store_nt = 0;
-    const int rgrid = int(std::max<int64_t>(1, std::min<int64_t>(ceil_div(r.per_split, 256), cu_count() * 8)));
     if (d->S == 0 || d->N == 0) {
         // Empty sums: every A[t, s] is +0 (N = 0) or there is no s at all,
         // so every output is +0 (operands are not read).
         r.nsplit = 0;
         r.partial = nullptr;
-        hipLaunchKernelGGL(splitk_reduce_kernel, dim3(rgrid), dim3(256), 0, s, r);
-        PE_CHECK_HIP(hipGetLastError());
+        PE_CHECK_HIP(launch_splitk_reduce(r, s));
         return PE_OK;
     }
     const Plan pl = plan(*d, q, k, m);
@@ -422,8 +467,7 @@ extern "C" int pe_linear_attention(const pe_linattn_desc* d, const void* q, cons
     if (pl.nsplit > 1) {
         r.nsplit = pl.nsplit;
         r.partial = reinterpret_cast<const float*>(wsb);
-        hipLaunchKernelGGL(splitk_reduce_kernel, dim3(rgrid), dim3(256), 0, s, r);
-        PE_CHECK_HIP(hipGetLastError());
+        PE_CHECK_HIP(launch_splitk_reduce(r, s));
     }
     return PE_OK;
 }
