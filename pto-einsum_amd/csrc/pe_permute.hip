@@ -54,9 +54,8 @@ struct Chunk {
     W v[VEC];
 };
 
-template <typename V>
-__device__ __forceinline__ void put(V* p, const V& v, bool nt) {
-    if (nt) __builtin_nontemporal_store(v, p);
+__device__ __forceinline__ void put(u32x4* p, const u32x4& v, bool nt) {
+    if (nt) store_nt(p, v);
     else *p = v;
 }
 
