@@ -16,6 +16,10 @@ microseconds, less than one Python-level call costs, so each is captured once
 in a HIP graph and the graph is replayed between two events: the figure is the
 GPU time of the einsum's launches.
 
+``gdn`` times the GDN contraction set at the reference's sizes the same way,
+and ``gdn_stages`` two of its stage sequences issued eagerly (one Python call
+per launch) and replayed as one HIP graph (``pto_einsum.StageGraph``).
+
 ``roofline.traffic`` (HBM bytes per launch of the headline GEMM) is read from
 profiles/gemm_f32_config2_traffic.json, written from two rocprofv3 --pmc runs
 (FETCH_SIZE, WRITE_SIZE) of this script, scaled by the same counters on
@@ -265,6 +269,125 @@ def time_fused_chain(dev, steps, warmup):
                 roof="mfma", frac=round(floor_ms / km, 4))
 
 
+GDN_EQS = (("kkt", "bihd,bjhd->bihj"), ("wy_fast", "bihj,bjhd->bihd"),
+           ("chunk_h kv", "bvhd,bvhe->bhde"), ("chunk_o inter", "bvhd,bhde->bvhe"))
+
+
+def gdn_list():
+    """The GDN contraction set (float32, chunk = d = 128) at the sizes the
+    reference measures it on (IMPLEMENTATION.md:700-782: b x H = 16x16, 64x16,
+    16x48; b = folded chunks): (label, equation, shape0, shape1)."""
+    rows = []
+    for b, H in ((16, 16), (64, 16), (16, 48)):
+        for name, eq in GDN_EQS:
+            s1 = (b, H, 128, 128) if eq == "bvhd,bhde->bvhe" else (b, 128, H, 128)
+            rows.append((f"{name} {b}x{H}", eq, (b, 128, H, 128), s1))
+    return rows
+
+
+def time_eager(fn, iters):
+    """GPU-side time (ms) per call of `fn` issued back to back from Python:
+    events around the whole loop, so host gaps between launches count."""
+    import torch
+
+    for _ in range(2):
+        fn()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(iters):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / iters
+
+
+def time_stage_graph(fn, iters):
+    import torch
+
+    from pto_einsum import StageGraph
+
+    graph = StageGraph(fn)
+    graph.replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(iters):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    del graph
+    return e0.elapsed_time(e1) / iters
+
+
+def time_gdn(dev, steps, warmup):
+    """Per-contraction GPU times of the GDN set, then two stage sequences
+    issued eagerly (one Python call per launch) and as one StageGraph replay:
+    the seven folded-batch contractions of one GDN forward (b = 16, H = 16)
+    and the chunk_h recurrence (B = 1, T = 1024, H = 32: per chunk two
+    contractions and four elementwise ops, eight chunks in sequence)."""
+    import torch
+
+    from pto_einsum import EinsumBuilder, einsum
+
+    rows = []
+    for label, eq, s0, s1 in gdn_list():
+        g = torch.Generator().manual_seed(200 + len(rows))
+        x = (torch.randn(s0, generator=g) * 128 ** -0.5).to(dev)
+        y = (torch.randn(s1, generator=g) * 128 ** -0.5).to(dev)
+        r = EinsumBuilder(eq, [s0, s1], torch.float32).build()
+        f, nb = work(eq, x, y)
+        km = time_graph(r, x, y, max(10, steps), max(3, warmup // 2), r(x, y).numel() * 4)
+        rf, tf, gb = roofline(f, nb, km, "f32")
+        rows.append(dict(gdn=label, equation=eq, dtype="f32", shapes=[list(s0), list(s1)], us=round(km * 1e3, 2),
+                         tflops=round(tf, 3), gbs=round(gb, 1), roof=rf["bound"], frac=rf["frac"]))
+        log(f"bench: gdn {label} {eq} {km * 1e3:.1f} us  {tf:.2f} TFLOP/s  {gb:.0f} GB/s  "
+            f"{rf['bound']} {rf['frac'] * 100:.1f}%")
+        del x, y, r
+
+    g = torch.Generator().manual_seed(300)
+    shape = (16, 128, 16, 128)
+    q, k, v = ((torch.randn(shape, generator=g) * 128 ** -0.5).to(dev) for _ in range(3))
+
+    def stages():
+        A = einsum("bihd,bjhd->bihj", k, k)
+        return (A, einsum("bihj,bjhd->bihd", A, v), einsum("bihj,bjhd->bihd", A, k),
+                einsum("bvhd,bhde->bvhe", q, einsum("bvhd,bvhe->bhde", k, v)),
+                einsum("bihj,bjhd->bihd", einsum("bihd,bjhd->bihj", q, k), v))
+
+    B, T, H, D = 1, 1024, 32, 128
+    w = (torch.randn(B, T, H, D, generator=g) * D ** -0.5).to(dev)
+    u = torch.randn(B, T, H, D, generator=g).to(dev)
+    kk = (torch.randn(B, T, H, D, generator=g) * D ** -0.5).to(dev)
+    gexp = (0.5 + 0.5 * torch.rand(B, T, H, 1, generator=g)).to(dev)
+    gdecay = (0.5 + 0.5 * torch.rand(T // 128, B, H, 1, 1, generator=g)).to(dev)
+    S0 = torch.zeros(B, H, D, D, device=dev)
+
+    def chunk_h():
+        S = S0
+        vs = []
+        for c in range(T // 128):
+            rows_ = slice(c * 128, (c + 1) * 128)
+            vc = u[:, rows_] - einsum("bvhd,bhde->bvhe", w[:, rows_], S)
+            vs.append(vc)
+            S = gdecay[c] * S + einsum("bvhd,bvhe->bhde", kk[:, rows_], vc * gexp[:, rows_])
+        return torch.cat(vs, dim=1), S
+
+    seqs = []
+    for label, fn, launches in (("gdn forward contractions b=16 H=16 (7 einsums)", stages, 7),
+                                ("chunk_h recurrence B=1 T=1024 H=32 (16 einsums + 32 elementwise)", chunk_h, 48)):
+        eager = time_eager(fn, max(10, steps))
+        replay = time_stage_graph(fn, max(10, steps))
+        seqs.append(dict(stages=label, launches=launches, eager_us=round(eager * 1e3, 2),
+                         graph_us=round(replay * 1e3, 2), speedup=round(eager / replay, 2)))
+        log(f"bench: {label}: eager {eager * 1e3:.1f} us, graph replay {replay * 1e3:.1f} us "
+            f"({eager / replay:.2f}x)")
+    torch.cuda.empty_cache()
+    return rows, seqs
+
+
 def rope_table(s, d):
     import torch
 
@@ -401,6 +524,7 @@ def main():
             f"dense-equivalent, mfma {fused['frac'] * 100:.1f}%); the three einsums take {chain_us:.1f} us")
 
     transposes = [] if args.no_configs else time_transposes(dev, args.steps, args.warmup)
+    gdn, gdn_stages = ([], []) if args.no_configs else time_gdn(dev, args.steps, args.warmup)
 
     log("bench: timing the CPU baseline")
     cpu = cpu_baseline(args.cpu_sample_batches, args.cpu_seconds)
@@ -425,6 +549,8 @@ def main():
         "cpu_baseline": cpu,
         "per_config": per_config,
         "transposes": transposes,
+        "gdn": gdn,
+        "gdn_stages": gdn_stages,
     }
     print(json.dumps(line), flush=True)
 

@@ -15,6 +15,10 @@
 #ifndef PE_GEMM_BIG
 #define PE_GEMM_BIG 1
 #endif
+// 128x128 tiles per CU at or below which 64x64 tiles are used instead.
+#ifndef PE_GEMM_SMALL_TILE_CUS
+#define PE_GEMM_SMALL_TILE_CUS 2
+#endif
 #ifndef PE_GEMM_BIG_PERSIST
 #define PE_GEMM_BIG_PERSIST -1
 #endif
@@ -117,8 +121,13 @@ GemmChoice choose(const pe_gemm_desc& d) {
         c.bn = d.M >= d.N ? 128 : d.tile;
         c.persist = PE_GEMM_BIG_PERSIST;
     } else {
+        // 64x64 unless 128x128 tiles give every CU more than two: with two
+        // or fewer per CU the smaller tiles' extra parallelism hides more
+        // load latency than their lower MFMA density costs (measured on
+        // MI355X for batched 128^3 blocks and 2048^2 outputs at K = 128..512).
         c.bm = (d.M > 64 && d.N > 64) ? 128 : 64;
-        if (c.bm == 128 && c.nbatch_total * ceil_div(d.M, 128) * ceil_div(d.N, 128) < cus) c.bm = 64;
+        if (c.bm == 128 && c.nbatch_total * ceil_div(d.M, 128) * ceil_div(d.N, 128) <= PE_GEMM_SMALL_TILE_CUS * cus)
+            c.bm = 64;
         c.bn = c.bm;
         if (PE_GEMM_BIG && c.bm == 128 && d.dtype == PE_F32) {
             // 256x128 / 128x256 tiles (wave tile 128x64) read fewer LDS
@@ -137,7 +146,11 @@ GemmChoice choose(const pe_gemm_desc& d) {
             const bool tall = d.M >= d.N;
             const int bbm = tall ? 256 : 128, bbn = tall ? 128 : 256;
             const int64_t bt = c.nbatch_total * ceil_div(d.M, bbm) * ceil_div(d.N, bbn);
-            if (bt >= cus && fill(bbm, bbn) >= PE_GEMM_BIG_MIN_FILL) {
+            // ... and only when they cover no more padding than 128x128
+            // tiles (a 128-row batch in a 256-row tile doubles the MFMAs).
+            const bool no_waste = ceil_div(d.M, bbm) * bbm * ceil_div(d.N, bbn) * bbn <=
+                                  ceil_div(d.M, 128) * 128 * ceil_div(d.N, 128) * 128;
+            if (bt >= cus && no_waste && fill(bbm, bbn) >= PE_GEMM_BIG_MIN_FILL) {
                 c.bm = bbm;
                 c.bn = bbn;
                 c.persist = PE_GEMM_BIG_PERSIST;

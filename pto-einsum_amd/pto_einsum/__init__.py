@@ -9,6 +9,7 @@ Public API, unchanged from the reference (src/pto_einsum/__init__.py:12-15):
 Beyond the reference's surface:
 
     linear_attention(q, k, v, m)            -> fused einsum("tn,sn,sp,ts->tp"), float32
+    StageGraph(fn)                          -> fn's launches captured into one HIP graph
 
 Example:
     >>> from pto_einsum import einsum
@@ -16,7 +17,8 @@ Example:
 """
 
 from .builder import EinsumBuilder, INCLUDE_DIR, einsum
+from .graph import StageGraph
 from .linattn import linear_attention
 
-__all__ = ["einsum", "EinsumBuilder", "INCLUDE_DIR", "linear_attention"]
+__all__ = ["einsum", "EinsumBuilder", "INCLUDE_DIR", "linear_attention", "StageGraph"]
 __version__ = "0.1.0"
