@@ -212,9 +212,6 @@ struct TileLoader {
 // B columns then meet in the same L2.  With fewer than 8 blocks, a plain
 // grid-stride order is used.  Every logical tile is visited exactly once
 // whatever XCD actually runs the block.
-#ifndef PE_GEMM_KROT
-#define PE_GEMM_KROT 0
-#endif
 #ifndef PE_GEMM_XCD_WALK
 #define PE_GEMM_XCD_WALK 1
 #endif
@@ -266,7 +263,7 @@ __global__ __launch_bounds__(kGemmThreads, 2) void gemm_kernel(GemmArgs g) {
         const T* B;
         int64_t c_off;
         uint32_t split, batch;
-        int m0, n0, rows_a, rows_b, k_len, rot;
+        int m0, n0, rows_a, rows_b, k_len;
     };
     auto locate = [&](uint32_t bid) {
         Tile x;
@@ -295,14 +292,6 @@ __global__ __launch_bounds__(kGemmThreads, 2) void gemm_kernel(GemmArgs g) {
         x.A = static_cast<const T*>(g.a) + a_off + int64_t(x.m0) * g.a_ms + int64_t(kb) * g.a_ks;
         x.B = static_cast<const T*>(g.b) + b_off + int64_t(x.n0) * g.b_ns + int64_t(kb) * g.b_ks;
         x.c_off = c_off;
-        x.rot = 0;
-        if (PE_GEMM_KROT && x.k_len % BK == 0) {
-            // Whole slabs only: start the k walk at a tile-dependent slab so
-            // tiles running side by side read different k columns.
-            x.rot = int(bid % uint32_t(x.k_len / BK));
-            x.A += int64_t(x.rot) * BK * g.a_ks;
-            x.B += int64_t(x.rot) * BK * g.b_ks;
-        }
         return x;
     };
 
@@ -340,10 +329,8 @@ __global__ __launch_bounds__(kGemmThreads, 2) void gemm_kernel(GemmArgs g) {
         for (int s = 0; s < nslabs; ++s) {
             const int cur = NBUF == 2 ? (s & 1) : 0;
             if (s + 1 < nslabs) {
-                // After the last slab of a rotated walk, wrap to slab 0.
-                const int64_t step = (s + 1 == nslabs - cur_t.rot) ? -int64_t(nslabs - 1) * BK : int64_t(BK);
-                A += step * g.a_ks;
-                B += step * g.b_ks;
+                A += int64_t(BK) * g.a_ks;
+                B += int64_t(BK) * g.b_ks;
                 la.load(A, g.a_ms, g.a_ks, rows_a, k_left - BK, tid);
                 lb.load(B, g.b_ns, g.b_ks, rows_b, k_left - BK, tid);
             }
