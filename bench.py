@@ -240,12 +240,14 @@ def time_transposes(dev, steps, warmup):
 def time_fused_chain(dev, steps, warmup):
     """BASELINE config 5's linear-attention chain in one fused launch
     (pto_einsum.linear_attention): q, k float16 normal(0, 1/sqrt(128)), v
-    float16 normal(0, 1) (read as float32), the causal decay mask
-    gamma^(t-s), gamma = 0.995, in float32; t = s = 4096, n = p = 128.  The
-    roof is the MFMA time of the chain's dense work: 2*T*S*N flops at the
-    float16 peak plus 2*T*S*P at the float32 peak (T*S mask multiplies on the
-    VALU are not counted against it).  Blocks of the mask that are zero are
-    skipped, so the causal case can beat the dense roof in principle."""
+    float16 normal(0, 1), the causal decay mask gamma^(t-s), gamma = 0.995,
+    in float32; t = s = 4096, n = p = 128.  The default launch computes P.V
+    as three bfloat16 MFMA terms of the split P and V; ``precise_us`` is the
+    same chain with P.V on float32 MFMAs.  The roof is the larger of the
+    compulsory HBM bytes (q, k, v, m read once, out written once) at 8 TB/s
+    and the MFMAs the default launch issues for the dense chain (2*T*S*N
+    float16 flops plus 3 * 2*T*S*P bfloat16 flops at the 16-bit peak); masked
+    blocks that are zero are skipped, so the causal case does less."""
     import torch
 
     from pto_einsum import linear_attention
@@ -261,12 +263,17 @@ def time_fused_chain(dev, steps, warmup):
     m = torch.where(d >= 0, 0.995 ** d.clamp(min=0), torch.zeros(())).float().to(dev)
     km = time_graph(lambda a, b: linear_attention(q, k, v, m), None, None, max(10, steps), max(3, warmup // 2),
                     T * P * 4)
+    kp = time_graph(lambda a, b: linear_attention(q, k, v, m, precise=True), None, None, max(10, steps),
+                    max(3, warmup // 2), T * P * 4)
     flops = 2 * T * S * N + T * S + 2 * T * S * P
     nbytes = (q.numel() + k.numel() + v.numel()) * 2 + m.numel() * 4 + T * P * 4
-    floor_ms = (2 * T * S * P / (PEAK_TFLOPS["f32"] * 1e12) + 2 * T * S * N / (PEAK_TFLOPS["f16"] * 1e12)) * 1e3
-    return dict(config="5.F", equation="tn,sn,sp,ts->tp (fused)", dtype="f16/f32", us=round(km * 1e3, 2),
-                tflops=round(flops / (km * 1e-3) / 1e12, 3), gbs=round(nbytes / (km * 1e-3) / 1e9, 1),
-                roof="mfma", frac=round(floor_ms / km, 4))
+    hbm_ms = nbytes / (PEAK_HBM_GBS * 1e9) * 1e3
+    mfma_ms = (2 * T * S * N + 3 * 2 * T * S * P) / (PEAK_TFLOPS["f16"] * 1e12) * 1e3
+    floor_ms = max(hbm_ms, mfma_ms)
+    return dict(config="5.F", equation="tn,sn,sp,ts->tp (fused)", dtype="f16 q/k, f32 chain (P.V as 3 bf16 terms)",
+                us=round(km * 1e3, 2), tflops=round(flops / (km * 1e-3) / 1e12, 3),
+                gbs=round(nbytes / (km * 1e-3) / 1e9, 1), roof="hbm" if hbm_ms >= mfma_ms else "mfma",
+                frac=round(floor_ms / km, 4), precise_us=round(kp * 1e3, 2))
 
 
 GDN_EQS = (("kkt", "bihd,bjhd->bihj"), ("wy_fast", "bihj,bjhd->bihd"),
@@ -521,7 +528,8 @@ def main():
         fused["three_einsums_us"] = round(chain_us, 2)
         per_config.append(fused)
         log(f"bench: config 5 fused tn,sn,sp,ts->tp {fused['us']:.1f} us ({fused['tflops']:.1f} TFLOP/s "
-            f"dense-equivalent, mfma {fused['frac'] * 100:.1f}%); the three einsums take {chain_us:.1f} us")
+            f"dense-equivalent, {fused['roof']} {fused['frac'] * 100:.1f}%; float32 P.V {fused['precise_us']:.1f} us); "
+            f"the three einsums take {chain_us:.1f} us")
 
     transposes = [] if args.no_configs else time_transposes(dev, args.steps, args.warmup)
     gdn, gdn_stages = ([], []) if args.no_configs else time_gdn(dev, args.steps, args.warmup)

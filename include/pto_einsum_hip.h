@@ -136,6 +136,11 @@ typedef struct pe_linattn_desc {
     int64_t T, S, N, P;
     int64_t q_ts, k_ss, v_ss, m_ts;     /* row strides, in elements */
     int64_t q_numel, k_numel, v_numel, m_numel;
+    int32_t precise;                    /* 1: P.V on float32 MFMAs; 0 (default): P and V split
+                                           into bfloat16 hi + lo, P.V as three bf16 MFMA terms
+                                           (products exact, float32 sums; each dropped term
+                                           below 2^-16 |P||V|) */
+    int32_t reserved;                   /* must be 0 */
 } pe_linattn_desc;
 
 int64_t pe_linear_attention_workspace_bytes(const pe_linattn_desc* d);

@@ -16,11 +16,17 @@
 //      s = 8*(r/4) + 4*(l/32) + r%4, r = 0..15.
 //   2. Those 16 values are multiplied by the mask in registers (one float32
 //      rounding, as the Hadamard step).
-//   3. They are exactly the A-operand registers of sixteen float32 MFMAs
-//      (v_mfma_f32_32x32x2_f32) whose k order is permuted to match: MFMA j
-//      pairs lane half h with s = 8*(j/4) + 4*h + j%4.  V is staged
-//      transposed in LDS so each lane reads its four consecutive s of one
-//      column p with one 16-byte read.
+//   3. P.V, by default on bfloat16 matrix cores: the 16 values are split into
+//      bfloat16 hi + lo (round to nearest even; x - hi is exact) and become
+//      the A operands of two v_mfma_f32_32x32x16_bf16 k-steps whose k order
+//      is permuted to match (step q2, lane half h, slot j <-> s = 16*q2 +
+//      8*(j/4) + 4*h + j%4).  V is split the same way when it is staged,
+//      transposed and in that permuted order, so one 16-byte LDS read gives a
+//      lane its eight k slots.  P.V = Phi.Vhi + Phi.Vlo + Plo.Vhi: products
+//      exact, sums float32, each dropped part below 2^-16 |P||V| (a float16 V
+//      splits exactly).  With `precise` the 16 values instead feed sixteen
+//      float32 MFMAs (v_mfma_f32_32x32x2_f32), MFMA j pairing lane half h with
+//      s = 8*(j/4) + 4*h + j%4, from a float32 transposed V tile.
 //
 // Blocks of 32 t x 32 s whose mask is zero everywhere are skipped: their
 // contribution is exactly +-0 for finite operands.  The s axis is split over
@@ -37,6 +43,7 @@
 #include "pe_gemm_kernel.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace pe {
 namespace {
@@ -44,7 +51,31 @@ namespace {
 constexpr int kTB = 128;       // t rows per block (four waves x 32)
 constexpr int kPB = 128;       // p columns per block (four 32-column MFMA blocks)
 constexpr int kSB = 32;        // s per step
-constexpr int kVLD = kSB + 4;  // LDS pitch of the transposed V tile (conflict-free 16-byte reads)
+constexpr int kVLD = kSB + 4;  // LDS pitch of the transposed float32 V tile (conflict-free 16-byte reads)
+constexpr int kVBLD = kSB + 8; // LDS pitch (bf16) of the split V tile: 80-byte rows, conflict-free 16-byte reads
+
+// V tile of one s step, transposed ([p][s]).  Float32 P.V: the float32
+// values.  Split P.V: V = hi + lo as two bfloat16 arrays whose s order is
+// permuted so that one 16-byte read gives a lane its eight k slots of a
+// 32x32x16 MFMA (see the P.V step).
+struct VTileF32 {
+    float v[kPB][kVLD];
+};
+struct VTileSplit {
+    uint16_t hi[kPB][kVBLD];
+    uint16_t lo[kPB][kVBLD];
+};
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+// Round-to-nearest-even split of a float32 into two bfloat16 terms: x = hi +
+// lo + e with |e| <= 2^-16 |x| (hi carries the top 8 significant bits, lo the
+// next 8; x - hi is exact in float32).
+__device__ __forceinline__ void split_bf16(float x, __bf16& hi, __bf16& lo) {
+    hi = __bf16(x);
+    lo = __bf16(x - float(hi));
+}
+__device__ __forceinline__ uint16_t bf16_bits(__bf16 x) { return __builtin_bit_cast(uint16_t, x); }
 
 struct LinAttnArgs {
     const void* q;
@@ -100,13 +131,14 @@ struct KTile {
 };
 
 // NSTEPS: MFMA k steps covering N (N <= NSTEPS * KSTEP); VE / ME: element
-// types of v and m.
+// types of v and m; PV32: P.V on float32 MFMAs (else on three bfloat16 MFMA
+// terms, hi*hi + hi*lo + lo*hi of the split P and V).
 //
 // Per s step (32 s), software-pipelined one step ahead: the V tile (32 x 128,
 // staged transposed), the K tile and this lane's mask values of step i+1 are
 // loaded into registers (raw element type, converted when committed) while
 // step i computes from LDS; two LDS stages mean one barrier per step.
-template <typename QK, int NSTEPS, typename VE, typename ME>
+template <typename QK, int NSTEPS, typename VE, typename ME, bool PV32>
 __global__ __launch_bounds__(256, 2) void linattn_kernel(LinAttnArgs a) {
     using T = typename QK::T;
     using VT = typename VE::T;
@@ -115,7 +147,8 @@ __global__ __launch_bounds__(256, 2) void linattn_kernel(LinAttnArgs a) {
     using KT = KTile<QK, NSTEPS>;
     using KChunk = typename Pack<KT::VEC, T>::type;
     using MV = typename Pack<4, MT>::type;
-    __shared__ __attribute__((aligned(16))) float vt[2][kPB][kVLD];          // V tile, transposed: [p][s]
+    using VTile = std::conditional_t<PV32, VTileF32, VTileSplit>;
+    __shared__ __attribute__((aligned(16))) VTile vt[2];                     // V tile, transposed: [p][s]
     __shared__ __attribute__((aligned(16))) T kt[2][kSB * KT::PITCH];       // K tile: [s][n]
 
     const int tid = threadIdx.x;
@@ -196,6 +229,34 @@ __global__ __launch_bounds__(256, 2) void linattn_kernel(LinAttnArgs a) {
         }
     };
 
+    // Writes this thread's 16 V values (s = vs0 .. vs0+15 of column vp) into
+    // a stage: float32, or split into bf16 hi / lo at the permuted positions
+    // 8*h + j <-> s = 8*(j/4) + 4*h + j%4 of the 16-s group.
+    auto commit_v = [&](int st, auto val) {
+        if constexpr (PV32) {
+#pragma unroll
+            for (int i = 0; i < 16; i += 4) {
+                f32x4 w = {val(i), val(i + 1), val(i + 2), val(i + 3)};
+                *reinterpret_cast<f32x4*>(&vt[st].v[vp][vs0 + i]) = w;
+            }
+        } else {
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                u32x4 wh, wl;
+#pragma unroll
+                for (int j = 0; j < 8; j += 2) {
+                    __bf16 h0, l0, h1, l1;
+                    split_bf16(val(8 * (j / 4) + 4 * hh + j % 4), h0, l0);
+                    split_bf16(val(8 * ((j + 1) / 4) + 4 * hh + (j + 1) % 4), h1, l1);
+                    wh[j / 2] = uint32_t(bf16_bits(h0)) | (uint32_t(bf16_bits(h1)) << 16);
+                    wl[j / 2] = uint32_t(bf16_bits(l0)) | (uint32_t(bf16_bits(l1)) << 16);
+                }
+                *reinterpret_cast<u32x4*>(&vt[st].hi[vp][vs0 + 8 * hh]) = wh;
+                *reinterpret_cast<u32x4*>(&vt[st].lo[vp][vs0 + 8 * hh]) = wl;
+            }
+        }
+    };
+
     if (s_begin < s_end) prefetch(s_begin);
     int stage = 0;
     for (int sb = s_begin; sb < s_end; sb += kSB, stage ^= 1) {
@@ -205,11 +266,7 @@ __global__ __launch_bounds__(256, 2) void linattn_kernel(LinAttnArgs a) {
         const bool full = sb + kSB <= a.S;
         float mv[16];
         if (full) {
-#pragma unroll
-            for (int i = 0; i < 16; i += 4) {
-                f32x4 w = {float(vpre[i]), float(vpre[i + 1]), float(vpre[i + 2]), float(vpre[i + 3])};
-                *reinterpret_cast<f32x4*>(&vt[stage][vp][vs0 + i]) = w;
-            }
+            commit_v(stage, [&](int i) { return float(vpre[i]); });
 #pragma unroll
             for (int i = 0; i < KT::PER_THREAD; ++i) {
                 const int c = tid + 256 * i;
@@ -221,13 +278,7 @@ __global__ __launch_bounds__(256, 2) void linattn_kernel(LinAttnArgs a) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) mv[4 * q + i] = float(mpre[q][i]);
         } else {
-#pragma unroll
-            for (int i = 0; i < 16; i += 4) {
-                f32x4 w;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) w[j] = sb + vs0 + i + j < a.S ? float(vpre[i + j]) : 0.0f;
-                *reinterpret_cast<f32x4*>(&vt[stage][vp][vs0 + i]) = w;
-            }
+            commit_v(stage, [&](int i) { return sb + vs0 + i < a.S ? float(vpre[i]) : 0.0f; });
 #pragma unroll
             for (int i = 0; i < KT::PER_THREAD; ++i) {
                 const int c = tid + 256 * i;
@@ -266,19 +317,48 @@ __global__ __launch_bounds__(256, 2) void linattn_kernel(LinAttnArgs a) {
             float av[16];
 #pragma unroll
             for (int r = 0; r < 16; ++r) av[r] = (sacc[0][r] + sacc[1][r]) * mv[r];
-            // 3. out[t, p] += sum_s A[t, s] v[s, p]; MFMA j takes s = 8*(j/4) + 4*h + j%4.
-            //    The four 32-column blocks are interleaved: four independent chains.
+            // 3. out[t, p] += sum_s A[t, s] v[s, p].  The four 32-column blocks
+            //    are interleaved: four independent chains.
+            if constexpr (PV32) {
+                // float32 MFMA j takes s = 8*(j/4) + 4*h + j%4.
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                f32x4 vf[4];
-#pragma unroll
-                for (int jb = 0; jb < 4; ++jb)
-                    vf[jb] = *reinterpret_cast<const f32x4*>(&vt[stage][32 * jb + l32][8 * q + 4 * h]);
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
+                for (int q = 0; q < 4; ++q) {
+                    f32x4 vf[4];
 #pragma unroll
                     for (int jb = 0; jb < 4; ++jb)
-                        acc[jb] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[4 * q + i], vf[jb][i], acc[jb], 0, 0, 0);
+                        vf[jb] = *reinterpret_cast<const f32x4*>(&vt[stage].v[32 * jb + l32][8 * q + 4 * h]);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+#pragma unroll
+                        for (int jb = 0; jb < 4; ++jb)
+                            acc[jb] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[4 * q + i], vf[jb][i], acc[jb], 0, 0, 0);
+                }
+            } else {
+                // bf16 32x32x16 MFMA step q2 covers s = 16*q2 .. 16*q2+15:
+                // lane half h, k slot j holds register r = 8*q2 + j, i.e.
+                // s = 16*q2 + 8*(j/4) + 4*h + j%4, matching the V positions.
+                // P.V = Phi.Vhi + Phi.Vlo + Plo.Vhi (products exact, float32
+                // sums; the dropped Plo.Vlo and the split remainders are each
+                // below 2^-16 |P||V|).
+#pragma unroll
+                for (int q2 = 0; q2 < 2; ++q2) {
+                    bf16x8 ph, pl;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        __bf16 x, y;
+                        split_bf16(av[8 * q2 + j], x, y);
+                        ph[j] = x;
+                        pl[j] = y;
+                    }
+#pragma unroll
+                    for (int jb = 0; jb < 4; ++jb) {
+                        const bf16x8 vh = *reinterpret_cast<const bf16x8*>(&vt[stage].hi[32 * jb + l32][16 * q2 + 8 * h]);
+                        const bf16x8 vl = *reinterpret_cast<const bf16x8*>(&vt[stage].lo[32 * jb + l32][16 * q2 + 8 * h]);
+                        acc[jb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ph, vh, acc[jb], 0, 0, 0);
+                        acc[jb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ph, vl, acc[jb], 0, 0, 0);
+                        acc[jb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pl, vh, acc[jb], 0, 0, 0);
+                    }
+                }
             }
         }
     }
@@ -352,6 +432,8 @@ int validate(const pe_linattn_desc& d) {
         return fail(PE_ERR_UNSUPPORTED, "linear_attention: dtypes must be PE_F32 or PE_F16");
     if (d.T < 0 || d.S < 0 || d.N < 0 || d.P < 0) return fail(PE_ERR_INVALID, "linear_attention: negative extent");
     if (d.split < 0) return fail(PE_ERR_INVALID, "linear_attention: split must be >= 0");
+    if (d.precise != 0 && d.precise != 1) return fail(PE_ERR_INVALID, "linear_attention: precise must be 0 or 1");
+    if (d.reserved != 0) return fail(PE_ERR_INVALID, "linear_attention: reserved field must be 0");
     const int64_t nmax = d.qk_dtype == PE_F16 ? 256 : 128;
     if (d.N > nmax) return fail(PE_ERR_UNSUPPORTED, "linear_attention: N above " + std::to_string(nmax));
     if (d.T >= (int64_t(1) << 31) || d.S >= (int64_t(1) << 31) || d.P >= (int64_t(1) << 31) ||
@@ -368,15 +450,19 @@ int validate(const pe_linattn_desc& d) {
 }
 
 template <typename QK, int NSTEPS, typename VE, typename ME>
-hipError_t launch(const LinAttnArgs& a, dim3 grid, hipStream_t s) {
-    hipLaunchKernelGGL((linattn_kernel<QK, NSTEPS, VE, ME>), grid, dim3(256), 0, s, a);
+hipError_t launch(const LinAttnArgs& a, bool pv32, dim3 grid, hipStream_t s) {
+    if (pv32)
+        hipLaunchKernelGGL((linattn_kernel<QK, NSTEPS, VE, ME, true>), grid, dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL((linattn_kernel<QK, NSTEPS, VE, ME, false>), grid, dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
 template <typename QK, int NSTEPS>
-hipError_t launch_vm(const LinAttnArgs& a, int vdt, int mdt, dim3 grid, hipStream_t s) {
-    if (vdt == PE_F16) return mdt == PE_F16 ? launch<QK, NSTEPS, F16, F16>(a, grid, s) : launch<QK, NSTEPS, F16, F32>(a, grid, s);
-    return mdt == PE_F16 ? launch<QK, NSTEPS, F32, F16>(a, grid, s) : launch<QK, NSTEPS, F32, F32>(a, grid, s);
+hipError_t launch_vm(const LinAttnArgs& a, int vdt, int mdt, bool pv32, dim3 grid, hipStream_t s) {
+    if (vdt == PE_F16)
+        return mdt == PE_F16 ? launch<QK, NSTEPS, F16, F16>(a, pv32, grid, s) : launch<QK, NSTEPS, F16, F32>(a, pv32, grid, s);
+    return mdt == PE_F16 ? launch<QK, NSTEPS, F32, F16>(a, pv32, grid, s) : launch<QK, NSTEPS, F32, F32>(a, pv32, grid, s);
 }
 
 hipError_t pad_rows(const void* src, int64_t stride, void* dst, int64_t rows, int64_t cols, int64_t pitch,
@@ -458,11 +544,12 @@ extern "C" int pe_linear_attention(const pe_linattn_desc* d, const void* q, cons
     a.s_per_split = pl.s_per_split;
     const dim3 grid(uint32_t(ceil_div(d->T, kTB)), uint32_t(ceil_div(d->P, kPB)), uint32_t(pl.nsplit));
     hipError_t e;
+    const bool pv32 = d->precise != 0;
     if (d->qk_dtype == PE_F16)
-        e = d->N <= 128 ? launch_vm<F16, 8>(a, d->v_dtype, d->m_dtype, grid, s)
-                        : launch_vm<F16, 16>(a, d->v_dtype, d->m_dtype, grid, s);
+        e = d->N <= 128 ? launch_vm<F16, 8>(a, d->v_dtype, d->m_dtype, pv32, grid, s)
+                        : launch_vm<F16, 16>(a, d->v_dtype, d->m_dtype, pv32, grid, s);
     else
-        e = launch_vm<F32, 64>(a, d->v_dtype, d->m_dtype, grid, s);
+        e = launch_vm<F32, 64>(a, d->v_dtype, d->m_dtype, pv32, grid, s);
     PE_CHECK_HIP(e);
     if (pl.nsplit > 1) {
         r.nsplit = pl.nsplit;

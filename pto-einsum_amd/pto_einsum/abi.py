@@ -55,7 +55,7 @@ class LinAttnDesc(ctypes.Structure):
                 ("q_ts", ctypes.c_int64), ("k_ss", ctypes.c_int64), ("v_ss", ctypes.c_int64),
                 ("m_ts", ctypes.c_int64),
                 ("q_numel", ctypes.c_int64), ("k_numel", ctypes.c_int64), ("v_numel", ctypes.c_int64),
-                ("m_numel", ctypes.c_int64)]
+                ("m_numel", ctypes.c_int64), ("precise", ctypes.c_int32), ("reserved", ctypes.c_int32)]
 
 
 def _set(arr, values: Sequence[int]):

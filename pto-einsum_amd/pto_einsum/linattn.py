@@ -17,6 +17,13 @@ keeps them in registers.  Results follow that chain's float32 arithmetic (every
 operand up-cast exactly, the inner sum and the mask product rounded to
 float32); sums are taken in a different order, so agreement is to contraction
 tolerance, not bit for bit.
+
+The last product P.V (P = the masked scores) runs by default on bfloat16
+matrix cores: P and V are each split into bfloat16 hi + lo (round to nearest
+even; x - hi is exact) and P.V = Phi.Vhi + Phi.Vlo + Plo.Vhi with exact
+products and float32 sums.  Each term left out (Plo.Vlo, the split remainders)
+is below 2^-16 |P||V|; a float16 V splits exactly.  ``precise=True`` runs P.V
+on float32 matrix cores instead (eight times the MFMA time of that product).
 """
 from __future__ import annotations
 
@@ -42,13 +49,15 @@ def _rows(t: torch.Tensor) -> torch.Tensor:
 
 
 def linear_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, m: torch.Tensor,
-                     *, split: int = 0) -> torch.Tensor:
+                     *, split: int = 0, precise: bool = False) -> torch.Tensor:
     """Fused ``einsum("tn,sn,sp,ts->tp", q, k, v, m)``; returns a float32
     [T, P] tensor on the operands' GPU.
 
     q [T, N] and k [S, N] share a dtype (float16 or float32; N <= 256 for
     float16, N <= 128 for float32); v [S, P] and m [T, S] are float16 or
-    float32.  ``split`` forces the number of s splits (0 = choose)."""
+    float32.  ``split`` forces the number of s splits (0 = choose);
+    ``precise`` computes P.V on float32 matrix cores instead of the split
+    bfloat16 terms."""
     for name, t in (("q", q), ("k", k), ("v", v), ("m", m)):
         if t.dim() != 2:
             raise ValueError(f"linear_attention: {name} must be 2-D, got shape {tuple(t.shape)}")
@@ -68,6 +77,7 @@ def linear_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, m: torch
 
     d = abi.LinAttnDesc()
     d.qk_dtype, d.v_dtype, d.m_dtype, d.split = _DT[q.dtype], _DT[v.dtype], _DT[m.dtype], int(split)
+    d.precise = 1 if precise else 0
     d.T, d.S, d.N, d.P = T, S, N, P
     d.q_ts, d.k_ss, d.v_ss, d.m_ts = q.stride(0), k.stride(0), v.stride(0), m.stride(0)
     d.q_numel, d.k_numel, d.v_numel, d.m_numel = (_extent(t) for t in (q, k, v, m))

@@ -86,8 +86,10 @@ STRUCT_PROBE = r"""
 #include "pto_einsum_hip.h"
 #define OFF(T, f) printf(#T "." #f " %zu\n", offsetof(T, f))
 int main() {
-  printf("pe_product_desc %zu\npe_permute_desc %zu\npe_gemm_desc %zu\npe_einsum_plan %zu\n",
-         sizeof(pe_product_desc), sizeof(pe_permute_desc), sizeof(pe_gemm_desc), sizeof(pe_einsum_plan));
+  printf("pe_product_desc %zu\npe_permute_desc %zu\npe_gemm_desc %zu\npe_einsum_plan %zu\npe_linattn_desc %zu\n",
+         sizeof(pe_product_desc), sizeof(pe_permute_desc), sizeof(pe_gemm_desc), sizeof(pe_einsum_plan),
+         sizeof(pe_linattn_desc));
+  OFF(pe_linattn_desc, m_numel); OFF(pe_linattn_desc, precise);
   OFF(pe_product_desc, b_numel); OFF(pe_permute_desc, src_numel); OFF(pe_gemm_desc, M);
   OFF(pe_gemm_desc, c_numel); OFF(pe_einsum_plan, gemm); OFF(pe_einsum_plan, ws_bytes);
   return 0;
@@ -112,6 +114,9 @@ def test_ctypes_struct_layout_matches_c(tmp_path):
     assert int(vals["pe_gemm_desc.c_numel"]) == abi.GemmDesc.c_numel.offset
     assert int(vals["pe_einsum_plan.gemm"]) == abi.EinsumPlan.gemm.offset
     assert int(vals["pe_einsum_plan.ws_bytes"]) == abi.EinsumPlan.ws_bytes.offset
+    assert int(vals["pe_linattn_desc"]) == ctypes.sizeof(abi.LinAttnDesc)
+    assert int(vals["pe_linattn_desc.m_numel"]) == abi.LinAttnDesc.m_numel.offset
+    assert int(vals["pe_linattn_desc.precise"]) == abi.LinAttnDesc.precise.offset
 
 
 def test_descriptor_validation_rejects_out_of_bounds():

@@ -56,14 +56,40 @@ def test_reference_chain_cases(dtype, T, S, N, P):
     (1, 1, 1, 1, torch.float16, torch.float16, torch.float16),
 ])
 @pytest.mark.parametrize("dense", [False, True], ids=["causal", "dense"])
-def test_shapes_and_dtypes(T, S, N, P, qk, vd, md, dense):
+@pytest.mark.parametrize("precise", [False, True], ids=["split_pv", "f32_pv"])
+def test_shapes_and_dtypes(T, S, N, P, qk, vd, md, dense, precise):
     g = torch.Generator().manual_seed(T * 7 + S)
     q = (torch.randn(T, N, generator=g) * N ** -0.5).to(qk)
     k = (torch.randn(S, N, generator=g) * N ** -0.5).to(qk)
     v = torch.randn(S, P, generator=g).to(vd)
     m = (torch.rand(T, S, generator=g) if dense else _decay(max(T, S), 0.97)[:T, :S]).to(md)
-    got = _run(q, k, v, m)
+    got = _run(q, k, v, m, precise=precise)
     check(got.numpy(), _want(q, k, v, m), False, RTOL[qk], "linear_attention")
+
+
+@pytest.mark.parametrize("vd", [torch.float16, torch.float32], ids=["v16", "v32"])
+def test_split_pv_error_bound(vd):
+    """The default P.V (bfloat16 hi/lo terms) against float32 MFMAs on the
+    same inputs, and both against a float64 evaluation: the split's error is
+    bounded by about 2^-15 sum_s |P||V| per output (three dropped terms below
+    2^-16 |P||V| each plus float32 rounding)."""
+    g = torch.Generator().manual_seed(50)
+    T, S, N, P = 512, 2048, 128, 128
+    q = (torch.randn(T, N, generator=g) * N ** -0.5).half()
+    k = (torch.randn(S, N, generator=g) * N ** -0.5).half()
+    v = (torch.randn(S, P, generator=g) * 3).to(vd)
+    m = _decay(S, 0.999)[:T]
+    split = _run(q, k, v, m)
+    f32 = _run(q, k, v, m, precise=True)
+    qc, kc, vc, mc = (x.cuda().double() for x in (q, k, v, m))
+    pm = (qc @ kc.T.contiguous()) * mc
+    ref = pm @ vc
+    bound = (pm.abs() @ vc.abs()) * 2.0 ** -15
+    err_split = (split.cuda().double() - ref).abs()
+    err_f32 = (f32.cuda().double() - ref).abs()
+    assert bool((err_split <= bound + 1e-30).all()), float((err_split / bound).max())
+    assert float(err_split.max()) <= 1e-5 * float(ref.abs().max())
+    assert float(err_f32.max()) <= 1e-5 * float(ref.abs().max())
 
 
 @pytest.mark.parametrize("split", [1, 2, 3, 7, 64])
