@@ -32,6 +32,11 @@
 
 #include "pe_common.h"
 
+// Float32 GEMMs whose operands qualify take the direct-load kernel.
+#ifndef PE_GEMM_DL
+#define PE_GEMM_DL 1
+#endif
+
 namespace pe {
 
 // Operand layout classes (chosen on the host from the strides).
@@ -91,6 +96,16 @@ int gemm_occupancy_f16(int bm, int bn);
 // < 0 = as many blocks per CU as the launched kernel keeps resident.
 hipError_t launch_gemm_f32(int bm, int bn, int alayout, int blayout, int persist, const GemmArgs& g,
                            hipStream_t s);
+// Direct-load float32 kernel (pe_gemm_dl.h): 64x64, 128x128, 256x128 and
+// 128x256 tiles, L_MN or L_K operands with the vector conditions
+// gemm_dl_eligible checks.  minb: register budget of the 256-wide tiles
+// (2 or 3 resident blocks per CU; 64x64 / 128x128 always use 4).
+// gemm_dl_resident returns the resident blocks per CU of one instantiation,
+// or 0 when the compiler spilled more than a few of its registers (never
+// launched).
+bool gemm_dl_eligible(int al, int bl, int64_t M, int64_t N, int64_t K);
+int gemm_dl_resident(int bm, int bn, int minb, int al, int bl);
+hipError_t launch_gemm_f32_dl(int bm, int bn, int minb, int al, int bl, const GemmArgs& g, hipStream_t s);
 hipError_t launch_gemm_f16(int bm, int bn, int alayout, int blayout, int persist, const GemmArgs& g,
                            hipStream_t s);
 

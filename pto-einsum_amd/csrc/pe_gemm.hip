@@ -95,6 +95,7 @@ namespace {
 
 struct GemmChoice {
     int bm, bn;    // tile: 64x64, 128x128, 256x128 or 128x256
+    int minb;      // direct-load kernel: register budget (resident blocks per CU) of 256-wide tiles
     int persist;   // blocks per CU of a persistent grid (0: one block per tile, -1: resident count)
     int nsplit;    // K splits (1 = direct store)
     int k_per_split;
@@ -108,8 +109,13 @@ int64_t batch_total(const pe_gemm_desc& d) {
     return n;
 }
 
-GemmChoice choose(const pe_gemm_desc& d) {
+// Direct-load operand layouts (dl = true) switch the 256-wide candidates to
+// the direct-load kernel's own instantiations.  The split-K decision and the
+// workspace size do not depend on it (256-wide tiles are only taken on grids
+// that need no split).
+GemmChoice choose(const pe_gemm_desc& d, bool dl = false, int al = L_MN, int bl = L_MN) {
     GemmChoice c{};
+    c.minb = 3;
     c.nbatch_total = batch_total(d);
     const int bk = gemm_bk(d.dtype);
     const int64_t cus = cu_count();
@@ -120,6 +126,7 @@ GemmChoice choose(const pe_gemm_desc& d) {
         c.bm = d.M >= d.N ? d.tile : 128;
         c.bn = d.M >= d.N ? 128 : d.tile;
         c.persist = PE_GEMM_BIG_PERSIST;
+        if (dl && gemm_dl_resident(c.bm, c.bn, 3, al, bl) < 1) c.minb = 2;
     } else {
         // 64x64 unless 128x128 tiles give every CU more than two: with two
         // or fewer per CU the smaller tiles' extra parallelism hides more
@@ -129,7 +136,42 @@ GemmChoice choose(const pe_gemm_desc& d) {
         if (c.bm == 128 && c.nbatch_total * ceil_div(d.M, 128) * ceil_div(d.N, 128) <= PE_GEMM_SMALL_TILE_CUS * cus)
             c.bm = 64;
         c.bn = c.bm;
-        if (PE_GEMM_BIG && c.bm == 128 && d.dtype == PE_F32) {
+        if (PE_GEMM_BIG && dl && c.bm == 128) {
+            // Direct-load 256x128 / 128x256 tiles come in two register
+            // budgets, three or two resident blocks per CU.  Like the tiles
+            // below they only pay off in whole rounds: config 2 (768 tiles)
+            // fills one round at three per CU, 4096^2 (512 tiles) one round
+            // at two per CU, where 512 blocks with three slots per CU left
+            // CUs with one block next to CUs with three (-18 %).  Measured
+            // on one MI355X for config 2: 346-354 us for the four 256-wide
+            // variants, 369 us for the staged kernel's 128x128 tiles.  Both
+            // orientations are candidates, the one along the longer output
+            // axis first (their register allocations differ; an
+            // instantiation that spills reports no residency).
+            double best = PE_GEMM_BIG_MIN_FILL;
+            bool taken = false;
+            const bool tall = d.M >= d.N;
+            for (int o = 0; o < 2; ++o) {
+                const bool wide_m = (o == 0) == tall;
+                const int bbm = wide_m ? 256 : 128, bbn = wide_m ? 128 : 256;
+                const int64_t bt = c.nbatch_total * ceil_div(d.M, bbm) * ceil_div(d.N, bbn);
+                const bool no_waste = ceil_div(d.M, bbm) * bbm * ceil_div(d.N, bbn) * bbn <=
+                                      ceil_div(d.M, 128) * 128 * ceil_div(d.N, 128) * 128;
+                for (int minb = 3; minb >= 2 && bt >= cus && no_waste; --minb) {
+                    const int res = gemm_dl_resident(bbm, bbn, minb, al, bl);
+                    if (res < 1) continue;
+                    const int64_t slots = cus * res;
+                    const double fill = double(bt) / double(ceil_div(bt, slots) * slots);
+                    if (fill >= best + 1e-9 || (fill >= best && !taken)) {
+                        best = fill;
+                        taken = true;
+                        c.bm = bbm;
+                        c.bn = bbn;
+                        c.minb = minb;
+                    }
+                }
+            }
+        } else if (PE_GEMM_BIG && c.bm == 128 && d.dtype == PE_F32) {
             // 256x128 / 128x256 tiles (wave tile 128x64) read fewer LDS
             // fragments per MFMA but hold two waves per SIMD.  Measured on
             // MI355X: they beat 128x128 by 10-25 % when their tiles fill the
@@ -267,16 +309,16 @@ extern "C" int pe_gemm(const pe_gemm_desc* d, const void* a, const void* b, floa
         return PE_OK;
     }
 
-    GemmChoice ch = choose(*d);
+    const int vec = d->dtype == PE_F32 ? 4 : 8;
+    const int al = classify(d->M, d->K, d->a_ms, d->a_ks, d->a_bstride, d->nbatch, a, vec);
+    const int bl = classify(d->N, d->K, d->b_ns, d->b_ks, d->b_bstride, d->nbatch, b, vec);
+    const bool dl = d->dtype == PE_F32 && d->tile != 192 && gemm_dl_eligible(al, bl, d->M, d->N, d->K);
+    GemmChoice ch = choose(*d, dl, al, bl);
     if (ch.nsplit > 1) {
         if (!ws || ws_bytes < ch.ws_bytes) return fail(PE_ERR_WORKSPACE, "gemm: split-K workspace missing or too small");
         if (nb * d->M * d->N >= (int64_t(1) << 32))
             return fail(PE_ERR_UNSUPPORTED, "gemm: split-K output too large");
     }
-    const int vec = d->dtype == PE_F32 ? 4 : 8;
-    const int al = classify(d->M, d->K, d->a_ms, d->a_ks, d->a_bstride, d->nbatch, a, vec);
-    const int bl = classify(d->N, d->K, d->b_ns, d->b_ks, d->b_bstride, d->nbatch, b, vec);
-
     GemmArgs g{};
     g.a = a; g.b = b; g.c = c;
     g.partial = static_cast<float*>(ws);
@@ -299,8 +341,9 @@ extern "C" int pe_gemm(const pe_gemm_desc* d, const void* a, const void* b, floa
         g.b_bs[i] = d->b_bstride[i];
         g.c_bs[i] = d->c_bstride[i];
     }
-    hipError_t e = d->dtype == PE_F32 ? launch_gemm_f32(ch.bm, ch.bn, al, bl, ch.persist, g, s)
-                                      : launch_gemm_f16(ch.bm, ch.bn, al, bl, ch.persist, g, s);
+    hipError_t e = dl                   ? launch_gemm_f32_dl(ch.bm, ch.bn, ch.minb, al, bl, g, s)
+                   : d->dtype == PE_F32 ? launch_gemm_f32(ch.bm, ch.bn, al, bl, ch.persist, g, s)
+                                        : launch_gemm_f16(ch.bm, ch.bn, al, bl, ch.persist, g, s);
     PE_CHECK_HIP(e);
     if (ch.nsplit > 1) {
         r.nsplit = ch.nsplit;

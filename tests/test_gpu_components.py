@@ -173,3 +173,28 @@ def test_gemm_rejects_bad_tile():
     d.tile, d.dtype = 96, launch.DT_F32
     rc = lib.pe_gemm(ctypes.byref(abi.gemm_desc(d)), _ptr(x), _ptr(x), _ptr(x), None, 0, _stream())
     assert rc == -1 and "tile" in runtime.last_error()
+
+
+@pytest.mark.parametrize("layout_a,layout_b", [("mn", "mn"), ("k", "k"), ("mn", "k"), ("k", "mn")])
+@pytest.mark.parametrize("nbatch,M,N,K", [(96, 512, 512, 40), (64, 512, 512, 36), (48, 520, 264, 100)])
+def test_gemm_float32_grids_of_wide_tiles(layout_a, layout_b, nbatch, M, N, K):
+    """Grids large enough for the tile choice to consider the 256-wide
+    float32 tiles at both register budgets (768 tiles fill one round at three
+    blocks per CU, 512 one round at two), with every operand layout pairing,
+    K tails of 8 and 4, and (last case) partial tiles in M and N."""
+    g = torch.Generator().manual_seed(nbatch + M + K)
+    A = torch.randn(nbatch, M, K, generator=g)
+    B = torch.randn(nbatch, K, N, generator=g)
+    if layout_a == "mn":
+        a_buf, a_ms, a_ks = A.transpose(1, 2).contiguous(), 1, M
+    else:
+        a_buf, a_ms, a_ks = A.contiguous(), K, 1
+    if layout_b == "mn":
+        b_buf, b_ks, b_ns = B.contiguous(), N, 1
+    else:
+        b_buf, b_ks, b_ns = B.transpose(1, 2).contiguous(), 1, K
+    got = _gemm_direct(a_buf.reshape(-1).cuda(), b_buf.reshape(-1).cuda(), M, N, K, a_ms, a_ks, b_ks, b_ns,
+                       launch.DT_F32, nbatch=nbatch)
+    want = torch.bmm(A.double().cuda(), B.double().cuda()).cpu()
+    scale = float(want.abs().max())
+    assert float((got.double() - want).abs().max()) <= 1e-4 * scale
