@@ -109,6 +109,14 @@ int64_t batch_total(const pe_gemm_desc& d) {
     return n;
 }
 
+// Orientation of a 256-wide tile: along the longer output axis; for equal
+// extents along the output's contiguous axis, so each tile row written is
+// 1 KB of contiguous memory rather than 512 B.
+bool wide_along_m(const pe_gemm_desc& d) {
+    if (d.M != d.N) return d.M > d.N;
+    return d.c_ms < d.c_ns;
+}
+
 // Direct-load operand layouts (dl = true) switch the 256-wide candidates to
 // the direct-load kernel's own instantiations.  The split-K decision and the
 // workspace size do not depend on it (256-wide tiles are only taken on grids
@@ -123,8 +131,9 @@ GemmChoice choose(const pe_gemm_desc& d, bool dl = false, int al = L_MN, int bl 
     if (d.tile == 64 || d.tile == 128) {
         c.bm = c.bn = d.tile;
     } else if (d.tile == 192 || d.tile == 256) {
-        c.bm = d.M >= d.N ? d.tile : 128;
-        c.bn = d.M >= d.N ? 128 : d.tile;
+        const bool tall = wide_along_m(d);
+        c.bm = tall ? d.tile : 128;
+        c.bn = tall ? 128 : d.tile;
         c.persist = PE_GEMM_BIG_PERSIST;
         if (dl && gemm_dl_resident(c.bm, c.bn, 3, al, bl) < 1) c.minb = 2;
     } else {
@@ -150,7 +159,7 @@ GemmChoice choose(const pe_gemm_desc& d, bool dl = false, int al = L_MN, int bl 
             // instantiation that spills reports no residency).
             double best = PE_GEMM_BIG_MIN_FILL;
             bool taken = false;
-            const bool tall = d.M >= d.N;
+            const bool tall = wide_along_m(d);
             for (int o = 0; o < 2; ++o) {
                 const bool wide_m = (o == 0) == tall;
                 const int bbm = wide_m ? 256 : 128, bbn = wide_m ? 128 : 256;
@@ -185,7 +194,7 @@ GemmChoice choose(const pe_gemm_desc& d, bool dl = false, int al = L_MN, int bl 
                 const int64_t rounds = ceil_div(t, slots);
                 return double(t) / double(rounds * slots);
             };
-            const bool tall = d.M >= d.N;
+            const bool tall = wide_along_m(d);
             const int bbm = tall ? 256 : 128, bbn = tall ? 128 : 256;
             const int64_t bt = c.nbatch_total * ceil_div(d.M, bbm) * ceil_div(d.N, bbn);
             // ... and only when they cover no more padding than 128x128
