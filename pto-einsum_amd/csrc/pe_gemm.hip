@@ -10,6 +10,13 @@
 #ifndef PE_GEMM_PERSIST
 #define PE_GEMM_PERSIST -1
 #endif
+// float16 GEMMs launch one block per tile: blocks dispatched in tile order
+// keep the output rows being written in a compact window of HBM, where
+// persistent blocks drift apart (config 3, whose 2.15 GB output dominates:
+// 458 -> 427 us on one MI355X; 5.1 unchanged).
+#ifndef PE_GEMM_F16_PERSIST
+#define PE_GEMM_F16_PERSIST 0
+#endif
 // 256x128 / 128x256 tiles (wave tile 128x64) for grids that still fill the
 // GPU, with their own persistent block count.
 #ifndef PE_GEMM_BIG
@@ -352,7 +359,7 @@ extern "C" int pe_gemm(const pe_gemm_desc* d, const void* a, const void* b, floa
     }
     hipError_t e = dl                   ? launch_gemm_f32_dl(ch.bm, ch.bn, ch.minb, al, bl, g, s)
                    : d->dtype == PE_F32 ? launch_gemm_f32(ch.bm, ch.bn, al, bl, ch.persist, g, s)
-                                        : launch_gemm_f16(ch.bm, ch.bn, al, bl, ch.persist, g, s);
+                                        : launch_gemm_f16(ch.bm, ch.bn, al, bl, PE_GEMM_F16_PERSIST, g, s);
     PE_CHECK_HIP(e);
     if (ch.nsplit > 1) {
         r.nsplit = ch.nsplit;

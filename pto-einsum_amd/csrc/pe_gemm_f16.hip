@@ -29,6 +29,7 @@ static hipError_t go(const GemmArgs& g, int persist, hipStream_t s) {
         const uint32_t cap = uint32_t(cu_count()) * uint32_t(persist < 0 ? resident : persist);
         if (a.grid > cap) a.grid = cap;
     }
+    if (a.grid > 0x7fffffffu) a.grid = 0x7fffffffu;  // grid limit; the tile walk strides over the rest
     hipLaunchKernelGGL(kernel, dim3(a.grid), dim3(kGemmThreads), 0, s, a);
     return hipGetLastError();
 }
