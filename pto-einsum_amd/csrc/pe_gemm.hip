@@ -116,6 +116,20 @@ int64_t batch_total(const pe_gemm_desc& d) {
     return n;
 }
 
+// True when the GEMM's compulsory HBM traffic (operands once, float32 output
+// once, at 8 TB/s) takes longer than its MFMA work at the dtype's dense peak
+// (157.3 TFLOP/s float32, 2516.6 float16): the output write then sets the
+// time, and blocks are launched one per tile in tile order (a compact window
+// of output rows in flight) rather than as a persistent grid.
+bool hbm_bound(const pe_gemm_desc& d) {
+    const double nb = double(batch_total(d));
+    const double eb = d.dtype == PE_F32 ? 4.0 : 2.0;
+    const double bytes = nb * (double(d.M) * d.N * 4.0 + (double(d.M) + d.N) * d.K * eb);
+    const double flops = 2.0 * nb * double(d.M) * d.N * d.K;
+    const double peak = d.dtype == PE_F32 ? 157.3e12 : 2516.6e12;
+    return bytes / 8.0e12 > flops / peak;
+}
+
 // Orientation of a 256-wide tile: along the longer output axis; for equal
 // extents along the output's contiguous axis, so each tile row written is
 // 1 KB of contiguous memory rather than 512 B.
@@ -142,7 +156,8 @@ GemmChoice choose(const pe_gemm_desc& d, bool dl = false, int al = L_MN, int bl 
         c.bm = tall ? d.tile : 128;
         c.bn = tall ? 128 : d.tile;
         c.persist = PE_GEMM_BIG_PERSIST;
-        if (dl && gemm_dl_resident(c.bm, c.bn, 3, al, bl) < 1) c.minb = 2;
+        if (dl && gemm_dl_resident(d.dtype, c.bm, c.bn, 3, al, bl) < 1) c.minb = 2;
+        if (dl && gemm_dl_resident(d.dtype, c.bm, c.bn, c.minb, al, bl) < 1) c.bm = c.bn = 128;
     } else {
         // 64x64 unless 128x128 tiles give every CU more than two: with two
         // or fewer per CU the smaller tiles' extra parallelism hides more
@@ -152,7 +167,7 @@ GemmChoice choose(const pe_gemm_desc& d, bool dl = false, int al = L_MN, int bl 
         if (c.bm == 128 && c.nbatch_total * ceil_div(d.M, 128) * ceil_div(d.N, 128) <= PE_GEMM_SMALL_TILE_CUS * cus)
             c.bm = 64;
         c.bn = c.bm;
-        if (PE_GEMM_BIG && dl && c.bm == 128) {
+        if (PE_GEMM_BIG && dl && c.bm == 128 && !hbm_bound(d)) {
             // Direct-load 256x128 / 128x256 tiles come in two register
             // budgets, three or two resident blocks per CU.  Like the tiles
             // below they only pay off in whole rounds: config 2 (768 tiles)
@@ -174,7 +189,7 @@ GemmChoice choose(const pe_gemm_desc& d, bool dl = false, int al = L_MN, int bl 
                 const bool no_waste = ceil_div(d.M, bbm) * bbm * ceil_div(d.N, bbn) * bbn <=
                                       ceil_div(d.M, 128) * 128 * ceil_div(d.N, 128) * 128;
                 for (int minb = 3; minb >= 2 && bt >= cus && no_waste; --minb) {
-                    const int res = gemm_dl_resident(bbm, bbn, minb, al, bl);
+                    const int res = gemm_dl_resident(d.dtype, bbm, bbn, minb, al, bl);
                     if (res < 1) continue;
                     const int64_t slots = cus * res;
                     const double fill = double(bt) / double(ceil_div(bt, slots) * slots);
@@ -187,7 +202,7 @@ GemmChoice choose(const pe_gemm_desc& d, bool dl = false, int al = L_MN, int bl 
                     }
                 }
             }
-        } else if (PE_GEMM_BIG && c.bm == 128 && d.dtype == PE_F32) {
+        } else if (PE_GEMM_BIG && !dl && c.bm == 128 && d.dtype == PE_F32) {
             // 256x128 / 128x256 tiles (wave tile 128x64) read fewer LDS
             // fragments per MFMA but hold two waves per SIMD.  Measured on
             // MI355X: they beat 128x128 by 10-25 % when their tiles fill the
@@ -328,7 +343,7 @@ extern "C" int pe_gemm(const pe_gemm_desc* d, const void* a, const void* b, floa
     const int vec = d->dtype == PE_F32 ? 4 : 8;
     const int al = classify(d->M, d->K, d->a_ms, d->a_ks, d->a_bstride, d->nbatch, a, vec);
     const int bl = classify(d->N, d->K, d->b_ns, d->b_ks, d->b_bstride, d->nbatch, b, vec);
-    const bool dl = d->dtype == PE_F32 && d->tile != 192 && gemm_dl_eligible(al, bl, d->M, d->N, d->K);
+    const bool dl = d->tile != 192 && gemm_dl_eligible(d->dtype, al, bl, d->M, d->N, d->K);
     GemmChoice ch = choose(*d, dl, al, bl);
     if (ch.nsplit > 1) {
         if (!ws || ws_bytes < ch.ws_bytes) return fail(PE_ERR_WORKSPACE, "gemm: split-K workspace missing or too small");
@@ -357,7 +372,7 @@ extern "C" int pe_gemm(const pe_gemm_desc* d, const void* a, const void* b, floa
         g.b_bs[i] = d->b_bstride[i];
         g.c_bs[i] = d->c_bstride[i];
     }
-    hipError_t e = dl                   ? launch_gemm_f32_dl(ch.bm, ch.bn, ch.minb, al, bl, g, s)
+    hipError_t e = dl                   ? launch_gemm_dl(d->dtype, ch.bm, ch.bn, ch.minb, al, bl, !hbm_bound(*d), g, s)
                    : d->dtype == PE_F32 ? launch_gemm_f32(ch.bm, ch.bn, al, bl, ch.persist, g, s)
                                         : launch_gemm_f16(ch.bm, ch.bn, al, bl, PE_GEMM_F16_PERSIST, g, s);
     PE_CHECK_HIP(e);

@@ -1,8 +1,9 @@
-// Float32 batched GEMM with direct global -> LDS operand loads (gfx950).
+// Batched GEMM with direct global -> LDS operand loads (gfx950), float32
+// and float16 operands, float32 accumulation and output.
 //
-// Same contract and tile walk as gemm_kernel (pe_gemm_kernel.h), for the
-// float32 operands whose 16-byte vectors run along M / N (L_MN) or along K
-// (L_K).  What differs is how a slab reaches LDS:
+// Same contract and tile walk as gemm_kernel (pe_gemm_kernel.h), for operands
+// whose 16-byte vectors run along M / N (L_MN) or along K (L_K).  What
+// differs is how a slab reaches LDS:
 //
 //  * each wave issues global_load_lds_dwordx4: 64 lanes x 16 bytes land in one
 //    1 KB LDS chunk, lane p at byte 16 p, with no register staging and no
@@ -14,30 +15,37 @@
 //  * each lane reads its MFMA fragments for the next k step while the
 //    current step's MFMAs issue.
 //
-// LDS layouts per stage (one 16-deep slab):
-//   L_MN: [16][ROWS]  k-major; a chunk holds 256 / ROWS whole k rows; a
-//         fragment is one 32-lane contiguous read per k.
-//   L_K : [ROWS][16]  k contiguous, 16-byte groups XOR-swizzled by
-//         (row / 4) % 4, so the 16 lanes of one ds_read_b64 phase (rows
-//         r .. r+15 at one k) hit 16 distinct bank pairs.  A lane's load
-//         fetches the global group that its swizzled slot holds.
-// Both operands use the same k order inside a slab: lane half h = lane / 32
-// of MFMA step st consumes k = 8 h + st.
+// A slab is 64 bytes of k per row: 16 float32 (8 steps of
+// v_mfma_f32_32x32x2_f32) or 32 float16 (2 steps of v_mfma_f32_32x32x16_f16).
+// LDS layouts per stage:
+//   L_MN: [BK][ROWS] k-major.  float32 fragments are one 32-lane contiguous
+//         read per k.  float16 fragments (8 consecutive k of one row per
+//         lane) come from two ds_read_b64_tr_b16: within each 16-lane group,
+//         lane i receives element i % 4 of the 8-byte blocks addressed by
+//         lanes i / 4, 4 + i / 4, 8 + i / 4, 12 + i / 4, so lanes 4 j + q
+//         pointing at k row kb + j, columns n0 + 4 q give lane i the four k
+//         values of column n0 + i.  The 16-byte groups of a float16 k row
+//         are XOR-swizzled by 2 (k % 4), so the four rows of one such read
+//         fall in eight distinct groups (no bank conflicts).
+//   L_K : [ROWS][BK] k contiguous, 16-byte groups XOR-swizzled by
+//         (row / 4) % 4, so the lanes of one read phase (consecutive rows at
+//         one k) hit distinct banks.
+// A lane's load fetches the global vector that its swizzled slot holds.  Both
+// operands use the same k order inside a slab: lane half h = lane / 32 of MFMA
+// step st consumes k = 8 h + st (float32) or 16 st + 8 h + 0..7 (float16).
 //
 // Boundaries: rows past M / N load a clamped (in-bounds) vector and only
 // feed outputs that are never stored.  The K tail of a tile's last slab
 // loads clamped (in-bounds) data and is then overwritten with zeros in LDS
 // before any MFMA reads it, so no value from outside the operand reaches a
 // stored sum.  Host-side conditions (see gemm_dl_eligible): L_MN operands
-// need M (resp. N) % 4 == 0, L_K operands need K % 4 == 0 (and so every
-// split's k extent), both need 16-byte aligned vectors.
+// need M (resp. N) to be a whole number of 16-byte vectors, L_K operands K
+// (and so every split's k extent), and both 16-byte aligned vectors.
 #pragma once
 
 #include "pe_gemm_kernel.h"
 
 namespace pe {
-
-constexpr int kDlBK = 16;
 
 // Output stores as inline assembly as well: a compiler-issued store would be
 // a tracked vector-memory operation, and the compiler then waits for the
@@ -61,107 +69,180 @@ __device__ __forceinline__ void dma16(const float* gptr, const float* lds) {
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(gptr), "s"(l) : "memory", "m0");
 }
 
-// One operand's share of a slab: ROWS rows (m or n) x 16 k.  Stateless:
+// Per-type slab geometry and MFMA.
+template <typename E>
+struct DlMath;
+template <>
+struct DlMath<F32> {
+    static constexpr int BK = 16;     // k per slab (64 bytes)
+    static constexpr int STEPS = 8;   // MFMA k steps per slab
+    using Frag = float;
+    __device__ __forceinline__ static f32x16 mfma(Frag a, Frag b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+    }
+};
+template <>
+struct DlMath<F16> {
+    static constexpr int BK = 32;
+    static constexpr int STEPS = 2;
+    using Frag = f16x8;
+    __device__ __forceinline__ static f32x16 mfma(Frag a, Frag b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+    }
+};
+
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+
+// One operand's share of a slab: ROWS rows (m or n) x BK k.  Stateless:
 // per-lane offsets are recomputed from the lane index at each use, so no
 // register stays live across slabs for them.
-template <int ROWS, int LAYOUT>
+template <typename E, int ROWS, int LAYOUT>
 struct DlOperand {
+    using T = typename E::T;
     static_assert(LAYOUT == L_MN || LAYOUT == L_K, "direct loads need 16-byte vectors");
-    static constexpr int ELEMS = ROWS * kDlBK;   // floats per stage
-    static constexpr int NCHUNK = ELEMS / 256;   // 1 KB chunks, one wave instruction each
-    static constexpr int NI = NCHUNK / 4;        // instructions per wave per slab
+    static constexpr bool kF32 = E::kBytes == 4;
+    static constexpr int BK = DlMath<E>::BK;
+    static constexpr int EPV = 16 / E::kBytes;        // elements per 16-byte vector
+    static constexpr int ELEMS = ROWS * BK;           // elements per stage
+    static constexpr int NCHUNK = ELEMS * E::kBytes / 1024;  // 1 KB chunks, one wave instruction each
+    static constexpr int NI = NCHUNK / 4;             // instructions per wave per slab
     static_assert(NI >= 1 && NCHUNK % 4 == 0, "every wave issues whole chunks");
-    static constexpr int LPR = ROWS / 4;         // L_MN: lanes per k row
-    // Fragment ring: values of the current and the next MFMA step (L_MN
-    // reads one k per step; L_K reads k pairs, so two pairs are held).
-    static constexpr int RING = LAYOUT == L_MN ? 2 : 4;
+    static constexpr int LPR = ROWS / EPV;            // L_MN: lanes (vectors) per k row
+    static constexpr int KPC = 64 / LPR;              // L_MN: k rows per chunk
+    static_assert(kF32 || LAYOUT == L_K || LPR >= 8, "float16 k-major swizzle needs 8 vectors per row");
+    // Fragment ring.  float32: L_MN reads one k per step (current + next);
+    // L_K reads k pairs, so two pairs are held.  float16: one 8-element
+    // fragment per step (current + next).
+    static constexpr int RING = !kF32 ? 2 : (LAYOUT == L_MN ? 2 : 4);
+    using Frag = typename DlMath<E>::Frag;
+
+    // float16 k-major swizzle: logical 16-byte group g of k row k sits at
+    // g ^ (2 (k % 4)).
+    __device__ __forceinline__ static int kswz(int k) { return kF32 ? 0 : 2 * (k & 3); }
 
     // Issues the slab's loads into `stage`.  base: operand at (batch, tile
     // row 0, slab k 0); rows_left / k_left: valid extent from there.
-    __device__ __forceinline__ static void load(const float* base, int64_t rs, int64_t ks, int rows_left,
-                                                int k_left, float* stage, int lane, int wave) {
+    __device__ __forceinline__ static void load(const T* base, int64_t rs, int64_t ks, int rows_left,
+                                                int k_left, T* stage, int lane, int wave) {
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
             const int c = i * 4 + wave;
             int r, k;
             if constexpr (LAYOUT == L_MN) {
-                k = min(c * (256 / ROWS) + lane / LPR, k_left - 1);
-                r = min((lane % LPR) * 4, rows_left - 4);
+                const int kk = c * KPC + lane / LPR;
+                k = min(kk, k_left - 1);
+                r = min(((lane % LPR) ^ kswz(kk)) * EPV, rows_left - EPV);
             } else {
                 r = min(c * 16 + lane / 4, rows_left - 1);
-                k = min(4 * ((lane % 4) ^ (lane / 16)), k_left - 4);
+                k = min(EPV * ((lane % 4) ^ (lane / 16)), k_left - EPV);
             }
-            dma16(base + int64_t(r) * rs + int64_t(k) * ks, stage + c * 256);
+            dma16(reinterpret_cast<const float*>(base + int64_t(r) * rs + int64_t(k) * ks),
+                  reinterpret_cast<const float*>(stage + c * (1024 / E::kBytes)));
         }
     }
 
-    // Zeroes every k >= k_left of a stage (0 < k_left < 16).
-    __device__ __forceinline__ static void zero_tail(float* stage, int k_left, int tid) {
+    // Zeroes every k >= k_left of a stage (0 < k_left < BK).
+    __device__ __forceinline__ static void zero_tail(T* stage, int k_left, int tid) {
         const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
         if constexpr (LAYOUT == L_MN) {
-            const int n = (kDlBK - k_left) * LPR;
+            const int n = (BK - k_left) * LPR;
             for (int idx = tid; idx < n; idx += kGemmThreads) {
-                const int k = k_left + idx / LPR, c = (idx % LPR) * 4;
+                const int k = k_left + idx / LPR, c = (idx % LPR) * EPV;
                 *reinterpret_cast<f32x4*>(stage + k * ROWS + c) = z;
             }
         } else {
             for (int idx = tid; idx < ROWS * 4; idx += kGemmThreads) {
                 const int r = idx / 4, pc = idx % 4;
                 const int lc = pc ^ ((r >> 2) & 3);
-                if (4 * lc >= k_left) *reinterpret_cast<f32x4*>(stage + r * 16 + pc * 4) = z;
+                if (EPV * lc >= k_left) *reinterpret_cast<f32x4*>(stage + r * BK + pc * EPV) = z;
             }
         }
     }
 
-    // Per-lane fragment offsets (floats from the stage origin) for a wave
-    // whose fragment rows start at wrow0: L_MN needs one, L_K one per half
-    // slab (the swizzled group of k = 8 h + 4 q differs per lane).
+    // Per-lane fragment offsets (elements from the stage origin) for a wave
+    // whose fragment rows start at wrow0 (a multiple of 32).
+    //   float32 L_MN: o[0]; float32 L_K: o[q] per half slab (the swizzled
+    //   group of k = 8 h + 4 q); float16 L_K: o[st] per step (group 2 st + h);
+    //   float16 L_MN: o[par] for fragment blocks whose 8-column group index
+    //   (wrow0 + 32 i) / 8 has bit 2 clear (par 0) or set (par 1), which the
+    //   XOR swizzle folds into the lane's group.
     struct LaneOff {
         int o[2];
     };
     __device__ __forceinline__ static LaneOff lane_off(int lane, int wrow0) {
         const int h = lane >> 5, r = wrow0 + (lane & 31);
         LaneOff x;
-        if constexpr (LAYOUT == L_MN) {
+        if constexpr (kF32 && LAYOUT == L_MN) {
             x.o[0] = 8 * h * ROWS + r;
             x.o[1] = 0;
-        } else {
+        } else if constexpr (kF32) {
+            // half slab q: lane half h owns k = 8 h .. 8 h + 7, groups 2 h + q
 #pragma unroll
-            for (int q = 0; q < 2; ++q) x.o[q] = r * 16 + (((2 * h + q) ^ ((r >> 2) & 3)) * 4);
+            for (int q = 0; q < 2; ++q) x.o[q] = r * BK + (((2 * h + q) ^ ((r >> 2) & 3)) * EPV);
+        } else if constexpr (LAYOUT == L_K) {
+            // step st: k = 16 st + 8 h .. + 7, group 2 st + h
+#pragma unroll
+            for (int st = 0; st < 2; ++st) x.o[st] = r * BK + (((2 * st + h) ^ ((r >> 2) & 3)) * EPV);
+        } else {
+            // Lane l of 16-lane group G = l / 16 points at k row 8 (G / 2) + j
+            // (j = (l % 16) / 4) and columns n0 + 4 q (n0 = 16 (G % 2),
+            // q = l % 4) of the fragment block; its 16-byte group is
+            // (C + 2 (G % 2) + q / 2) ^ 2 j with C = (wrow0 + 32 i) / 8.
+            const int G = lane >> 4, j = (lane & 15) >> 2, q = lane & 3;
+            const int zz = (2 * (G & 1) + (q >> 1)) ^ (2 * j);
+#pragma unroll
+            for (int par = 0; par < 2; ++par)
+                x.o[par] = (8 * (G >> 1) + j) * ROWS + 8 * (zz ^ (4 * par)) + 4 * (q & 1);
         }
         return x;
     }
 
-    // Reads what MFMA step st needs (lane half h consumes k = 8 h + st) for
-    // fragment block i (rows 32 i .. 32 i + 31 of the wave) into ring slot
-    // st % RING; L_K reads k pairs, at even steps only (slots st % 4 and
-    // (st + 1) % 4).  All offsets but the lane's are compile-time constants.
-    __device__ __forceinline__ static void frag(const float* stage, const LaneOff& lo, int i, int st,
-                                                float (&v)[RING]) {
-        if constexpr (LAYOUT == L_MN) {
+    // Reads what MFMA step st needs for fragment block i (rows 32 i ..
+    // 32 i + 31 of the wave, which starts at wrow0) into ring slot
+    // st % RING.  float32 L_K reads k pairs, at even steps only (slots st % 4
+    // and (st + 1) % 4).  All offsets but the lane's are uniform.
+    __device__ __forceinline__ static void frag(const T* stage, const LaneOff& lo, int wrow0, int i, int st,
+                                                Frag (&v)[RING]) {
+        if constexpr (kF32 && LAYOUT == L_MN) {
             v[st % 2] = stage[lo.o[0] + st * ROWS + i * 32];
-        } else if (st % 2 == 0) {
-            typedef float f32x2 __attribute__((ext_vector_type(2)));
-            const f32x2 x = *reinterpret_cast<const f32x2*>(stage + lo.o[st / 4] + i * 32 * 16 + st % 4);
-            v[st % 4] = x[0];
-            v[(st + 1) % 4] = x[1];
+        } else if constexpr (kF32) {
+            if (st % 2 == 0) {
+                typedef float f32x2 __attribute__((ext_vector_type(2)));
+                const f32x2 x = *reinterpret_cast<const f32x2*>(stage + lo.o[st / 4] + i * 32 * BK + st % 4);
+                v[st % 4] = x[0];
+                v[(st + 1) % 4] = x[1];
+            }
+        } else if constexpr (LAYOUT == L_K) {
+            v[st % 2] = *reinterpret_cast<const f16x8*>(stage + lo.o[st] + i * 32 * BK);
+        } else {
+            const int C = wrow0 / 8 + 4 * i;
+            const T* p = stage + lo.o[(C >> 2) & 1] + 8 * (C & ~7) + 16 * st * ROWS;
+            const i16x4 lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) i16x4*)(p));
+            const i16x4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) i16x4*)(p + 4 * ROWS));
+            typedef short i16x8 __attribute__((ext_vector_type(8)));
+            const i16x8 w = {lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+            v[st % 2] = __builtin_bit_cast(f16x8, w);
         }
     }
 };
 
 // MINB: resident blocks per CU the register allocation is held to (four
 // waves per block, one per SIMD, so MINB waves per SIMD).
-template <int BM, int BN, int AL, int BL, int MINB>
+template <typename E, int BM, int BN, int AL, int BL, int MINB>
 __global__ __launch_bounds__(kGemmThreads, MINB) void gemm_dl_kernel(GemmArgs g) {
-    using OA = DlOperand<BM, AL>;
-    using OB = DlOperand<BN, BL>;
-    constexpr int BK = kDlBK;
+    using T = typename E::T;
+    using M = DlMath<E>;
+    using OA = DlOperand<E, BM, AL>;
+    using OB = DlOperand<E, BN, BL>;
+    constexpr int BK = M::BK;
     constexpr int WM = BM / 2, WN = BN / 2;
     constexpr int FM = WM / 32, FN = WN / 32;
-    __shared__ __attribute__((aligned(16))) float sa0[OA::ELEMS];
-    __shared__ __attribute__((aligned(16))) float sa1[OA::ELEMS];
-    __shared__ __attribute__((aligned(16))) float sb0[OB::ELEMS];
-    __shared__ __attribute__((aligned(16))) float sb1[OB::ELEMS];
+    __shared__ __attribute__((aligned(16))) T sa0[OA::ELEMS];
+    __shared__ __attribute__((aligned(16))) T sa1[OA::ELEMS];
+    __shared__ __attribute__((aligned(16))) T sb0[OB::ELEMS];
+    __shared__ __attribute__((aligned(16))) T sb1[OB::ELEMS];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -171,8 +252,8 @@ __global__ __launch_bounds__(kGemmThreads, MINB) void gemm_dl_kernel(GemmArgs g)
     const uint32_t tiles_all = g.tiles_per_batch * g.nbatch_total;
 
     struct Tile {
-        const float* A;
-        const float* B;
+        const T* A;
+        const T* B;
         int64_t c_off;
         uint32_t split, batch;
         int m0, n0, rows_a, rows_b, k_len, nslabs;
@@ -202,8 +283,8 @@ __global__ __launch_bounds__(kGemmThreads, MINB) void gemm_dl_kernel(GemmArgs g)
         x.nslabs = (x.k_len + BK - 1) / BK;
         x.rows_a = g.M - x.m0;
         x.rows_b = g.N - x.n0;
-        x.A = static_cast<const float*>(g.a) + a_off + int64_t(x.m0) * g.a_ms + int64_t(kb) * g.a_ks;
-        x.B = static_cast<const float*>(g.b) + b_off + int64_t(x.n0) * g.b_ns + int64_t(kb) * g.b_ks;
+        x.A = static_cast<const T*>(g.a) + a_off + int64_t(x.m0) * g.a_ms + int64_t(kb) * g.a_ks;
+        x.B = static_cast<const T*>(g.b) + b_off + int64_t(x.n0) * g.b_ns + int64_t(kb) * g.b_ks;
         x.c_off = c_off;
         return x;
     };
@@ -221,7 +302,7 @@ __global__ __launch_bounds__(kGemmThreads, MINB) void gemm_dl_kernel(GemmArgs g)
     int ls = 0;              // its next slab to load
     bool lvalid = true;
 
-    auto issue = [&](float* da, float* db) {
+    auto issue = [&](T* da, T* db) {
         const int kl = lt.k_len - ls * BK;
         OA::load(lt.A + int64_t(ls) * BK * g.a_ks, g.a_ms, g.a_ks, lt.rows_a, kl, da, lane, wave);
         OB::load(lt.B + int64_t(ls) * BK * g.b_ks, g.b_ns, g.b_ks, lt.rows_b, kl, db, lane, wave);
@@ -278,29 +359,29 @@ __global__ __launch_bounds__(kGemmThreads, MINB) void gemm_dl_kernel(GemmArgs g)
 
     // One slab: wait for its loads, start the next slab's loads into the
     // other stage, then the MFMAs.  Returns true when the block is done.
-    auto step = [&](const float* sa, const float* sb, float* na, float* nb) -> bool {
+    auto step = [&](const T* sa, const T* sb, T* na, T* nb) -> bool {
         // This wave's loads of the slab have landed; after the barrier every
         // wave's have, and every wave is done reading the other stage.
         asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
         if (lvalid) issue(na, nb);
         const int k_left = ct.k_len - cs * BK;
         if (k_left < BK) {
-            OA::zero_tail(const_cast<float*>(sa), k_left, tid);
-            OB::zero_tail(const_cast<float*>(sb), k_left, tid);
+            OA::zero_tail(const_cast<T*>(sa), k_left, tid);
+            OB::zero_tail(const_cast<T*>(sb), k_left, tid);
             asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         }
-        float fa[FM][OA::RING], fb[FN][OB::RING];
+        typename M::Frag fa[FM][OA::RING], fb[FN][OB::RING];
 #pragma unroll
-        for (int i = 0; i < FM; ++i) OA::frag(sa, loa, i, 0, fa[i]);
+        for (int i = 0; i < FM; ++i) OA::frag(sa, loa, wm * WM, i, 0, fa[i]);
 #pragma unroll
-        for (int j = 0; j < FN; ++j) OB::frag(sb, lob, j, 0, fb[j]);
+        for (int j = 0; j < FN; ++j) OB::frag(sb, lob, wn * WN, j, 0, fb[j]);
 #pragma unroll
-        for (int st = 0; st < BK / 2; ++st) {
-            if (st + 1 < BK / 2) {
+        for (int st = 0; st < M::STEPS; ++st) {
+            if (st + 1 < M::STEPS) {
 #pragma unroll
-                for (int i = 0; i < FM; ++i) OA::frag(sa, loa, i, st + 1, fa[i]);
+                for (int i = 0; i < FM; ++i) OA::frag(sa, loa, wm * WM, i, st + 1, fa[i]);
 #pragma unroll
-                for (int j = 0; j < FN; ++j) OB::frag(sb, lob, j, st + 1, fb[j]);
+                for (int j = 0; j < FN; ++j) OB::frag(sb, lob, wn * WN, j, st + 1, fb[j]);
             }
             // Keep the next step's reads ahead of this step's MFMAs (the
             // scheduler would otherwise sink them to save registers and wait
@@ -310,8 +391,7 @@ __global__ __launch_bounds__(kGemmThreads, MINB) void gemm_dl_kernel(GemmArgs g)
             for (int i = 0; i < FM; ++i)
 #pragma unroll
                 for (int j = 0; j < FN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][st % OA::RING], fb[j][st % OB::RING],
-                                                                     acc[i][j], 0, 0, 0);
+                    acc[i][j] = M::mfma(fa[i][st % OA::RING], fb[j][st % OB::RING], acc[i][j]);
         }
         if (++cs == ct.nslabs) {
             epilogue();

@@ -1,0 +1,87 @@
+// Host side of the direct-load GEMM kernel (pe_gemm_dl.h): the
+// instantiations for float32 and float16, their residency (with the
+// register-spill check) and the launch.
+#include "pe_gemm_dl.h"
+
+namespace pe {
+
+// Direct-load kernels: 64x64 and 128x128 tiles held to four resident blocks
+// per CU, 256x128 / 128x256 tiles in two register budgets (two or three
+// resident blocks per CU; which one fits a grid is decided in choose()).
+template <typename E, int BM, int BN, int MINB>
+static const void* dl_kernel_ab(int al, int bl) {
+    if (al == L_MN)
+        return bl == L_MN ? reinterpret_cast<const void*>(&gemm_dl_kernel<E, BM, BN, L_MN, L_MN, MINB>)
+                          : reinterpret_cast<const void*>(&gemm_dl_kernel<E, BM, BN, L_MN, L_K, MINB>);
+    return bl == L_MN ? reinterpret_cast<const void*>(&gemm_dl_kernel<E, BM, BN, L_K, L_MN, MINB>)
+                      : reinterpret_cast<const void*>(&gemm_dl_kernel<E, BM, BN, L_K, L_K, MINB>);
+}
+
+template <typename E>
+static const void* dl_kernel_t(int bm, int bn, int minb, int al, int bl) {
+    if (bm == 256) return minb == 2 ? dl_kernel_ab<E, 256, 128, 2>(al, bl) : dl_kernel_ab<E, 256, 128, 3>(al, bl);
+    if (bn == 256) return minb == 2 ? dl_kernel_ab<E, 128, 256, 2>(al, bl) : dl_kernel_ab<E, 128, 256, 3>(al, bl);
+    return bm == 128 ? dl_kernel_ab<E, 128, 128, 4>(al, bl) : dl_kernel_ab<E, 64, 64, 4>(al, bl);
+}
+
+static const void* dl_kernel(int dtype, int bm, int bn, int minb, int al, int bl) {
+    return dtype == PE_F32 ? dl_kernel_t<F32>(bm, bn, minb, al, bl) : dl_kernel_t<F16>(bm, bn, minb, al, bl);
+}
+
+static int dl_index(int dtype, int bm, int bn, int minb, int al, int bl) {
+    const int t = bm == 256 ? (minb == 2 ? 2 : 3) : bn == 256 ? (minb == 2 ? 4 : 5) : bm == 128 ? 1 : 0;
+    return ((((dtype == PE_F32) ? 0 : 6) + t) * 2 + (al == L_K)) * 2 + (bl == L_K);
+}
+
+// Instantiations whose register allocation spilled more than this many bytes
+// per lane are never launched.  The 128x256 tile at three blocks per CU
+// spills one lane offset (8 bytes, reloaded once per slab) and runs config 2
+// as fast as the spill-free variants; larger spills sit inside the MFMA loop.
+#ifndef PE_GEMM_DL_MAX_SPILL
+#define PE_GEMM_DL_MAX_SPILL 16
+#endif
+
+int gemm_dl_resident(int dtype, int bm, int bn, int minb, int al, int bl) {
+    static int cache[2 * 6 * 4];
+    static bool init = false;
+    if (!init) {
+        for (int& c : cache) c = -1;
+        init = true;
+    }
+    int& c = cache[dl_index(dtype, bm, bn, minb, al, bl)];
+    if (c < 0) {
+        const void* k = dl_kernel(dtype, bm, bn, minb, al, bl);
+        hipFuncAttributes at{};
+        int n = 0;
+        if (hipFuncGetAttributes(&at, k) != hipSuccess || at.localSizeBytes > PE_GEMM_DL_MAX_SPILL ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k, kGemmThreads, 0) != hipSuccess || n < 1)
+            n = 0;
+        c = n;
+    }
+    return c;
+}
+
+bool gemm_dl_eligible(int dtype, int al, int bl, int64_t M, int64_t N, int64_t K) {
+    if (!PE_GEMM_DL) return false;
+    if (dtype == PE_F16 && !PE_GEMM_DL_F16) return false;
+    const int vec = dtype == PE_F32 ? 4 : 8;  // elements per 16-byte vector
+    if (al != L_MN && al != L_K) return false;
+    if (bl != L_MN && bl != L_K) return false;
+    if (al == L_MN && M % vec != 0) return false;
+    if (bl == L_MN && N % vec != 0) return false;
+    if ((al == L_K || bl == L_K) && K % vec != 0) return false;
+    return true;
+}
+
+hipError_t launch_gemm_dl(int dtype, int bm, int bn, int minb, int al, int bl, bool persist, const GemmArgs& g,
+                          hipStream_t s) {
+    const int resident = gemm_dl_resident(dtype, bm, bn, minb, al, bl);
+    if (resident < 1) return hipErrorInvalidConfiguration;
+    GemmArgs a = g;
+    const uint32_t cap = persist ? uint32_t(cu_count()) * uint32_t(resident) : 0x7fffffffu;
+    if (a.grid > cap) a.grid = cap;
+    void* args[] = {&a};
+    return hipLaunchKernel(dl_kernel(dtype, bm, bn, minb, al, bl), dim3(a.grid), dim3(kGemmThreads), args, 0, s);
+}
+
+}  // namespace pe

@@ -1,5 +1,5 @@
 // float32 instantiations of the batched MFMA GEMM (v_mfma_f32_32x32x2_f32).
-#include "pe_gemm_dl.h"
+#include "pe_gemm_kernel.h"
 
 // Slab depth and LDS layout for float32 (see GemmGeom).
 #ifndef PE_GEMM_F32_BK
@@ -76,77 +76,6 @@ int gemm_occupancy_f32(int bm, int bn) {
     if (bm == 192) return o[4];
     if (bn == 192) return o[5];
     return bm == 128 ? o[1] : o[0];
-}
-
-// Direct-load kernels: 64x64 and 128x128 tiles held to four resident blocks
-// per CU, 256x128 / 128x256 tiles in two register budgets (two or three
-// resident blocks per CU; which one fits a grid is decided in choose()).
-template <int BM, int BN, int MINB>
-static const void* dl_kernel_ab(int al, int bl) {
-    if (al == L_MN)
-        return bl == L_MN ? reinterpret_cast<const void*>(&gemm_dl_kernel<BM, BN, L_MN, L_MN, MINB>)
-                          : reinterpret_cast<const void*>(&gemm_dl_kernel<BM, BN, L_MN, L_K, MINB>);
-    return bl == L_MN ? reinterpret_cast<const void*>(&gemm_dl_kernel<BM, BN, L_K, L_MN, MINB>)
-                      : reinterpret_cast<const void*>(&gemm_dl_kernel<BM, BN, L_K, L_K, MINB>);
-}
-
-static const void* dl_kernel(int bm, int bn, int minb, int al, int bl) {
-    if (bm == 256) return minb == 2 ? dl_kernel_ab<256, 128, 2>(al, bl) : dl_kernel_ab<256, 128, 3>(al, bl);
-    if (bn == 256) return minb == 2 ? dl_kernel_ab<128, 256, 2>(al, bl) : dl_kernel_ab<128, 256, 3>(al, bl);
-    return bm == 128 ? dl_kernel_ab<128, 128, 4>(al, bl) : dl_kernel_ab<64, 64, 4>(al, bl);
-}
-
-static int dl_index(int bm, int bn, int minb, int al, int bl) {
-    const int t = bm == 256 ? (minb == 2 ? 2 : 3) : bn == 256 ? (minb == 2 ? 4 : 5) : bm == 128 ? 1 : 0;
-    return (t * 2 + (al == L_K)) * 2 + (bl == L_K);
-}
-
-// Instantiations whose register allocation spilled more than this many bytes
-// per lane are never launched.  The 128x256 tile at three blocks per CU
-// spills one lane offset (8 bytes, reloaded once per slab) and runs config 2
-// as fast as the spill-free variants; larger spills sit inside the MFMA loop.
-#ifndef PE_GEMM_DL_MAX_SPILL
-#define PE_GEMM_DL_MAX_SPILL 16
-#endif
-
-int gemm_dl_resident(int bm, int bn, int minb, int al, int bl) {
-    static int cache[6 * 4];
-    static bool init = false;
-    if (!init) {
-        for (int& c : cache) c = -1;
-        init = true;
-    }
-    int& c = cache[dl_index(bm, bn, minb, al, bl)];
-    if (c < 0) {
-        const void* k = dl_kernel(bm, bn, minb, al, bl);
-        hipFuncAttributes at{};
-        int n = 0;
-        if (hipFuncGetAttributes(&at, k) != hipSuccess || at.localSizeBytes > PE_GEMM_DL_MAX_SPILL ||
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k, kGemmThreads, 0) != hipSuccess || n < 1)
-            n = 0;
-        c = n;
-    }
-    return c;
-}
-
-bool gemm_dl_eligible(int al, int bl, int64_t M, int64_t N, int64_t K) {
-    if (!PE_GEMM_DL) return false;
-    if (al != L_MN && al != L_K) return false;
-    if (bl != L_MN && bl != L_K) return false;
-    if (al == L_MN && M % 4 != 0) return false;
-    if (bl == L_MN && N % 4 != 0) return false;
-    if ((al == L_K || bl == L_K) && K % 4 != 0) return false;
-    return true;
-}
-
-hipError_t launch_gemm_f32_dl(int bm, int bn, int minb, int al, int bl, const GemmArgs& g, hipStream_t s) {
-    const int resident = gemm_dl_resident(bm, bn, minb, al, bl);
-    if (resident < 1) return hipErrorInvalidConfiguration;
-    GemmArgs a = g;
-    const uint32_t cap = uint32_t(cu_count()) * uint32_t(resident);
-    if (a.grid > cap) a.grid = cap;
-    void* args[] = {&a};
-    return hipLaunchKernel(dl_kernel(bm, bn, minb, al, bl), dim3(a.grid), dim3(kGemmThreads), args, 0, s);
 }
 
 hipError_t launch_gemm_f32(int bm, int bn, int al, int bl, int persist, const GemmArgs& g,
