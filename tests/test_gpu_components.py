@@ -176,15 +176,22 @@ def test_gemm_rejects_bad_tile():
 
 
 @pytest.mark.parametrize("layout_a,layout_b", [("mn", "mn"), ("k", "k"), ("mn", "k"), ("k", "mn")])
-@pytest.mark.parametrize("nbatch,M,N,K", [(96, 512, 512, 40), (64, 512, 512, 36), (48, 520, 264, 100)])
-def test_gemm_float32_grids_of_wide_tiles(layout_a, layout_b, nbatch, M, N, K):
-    """Grids large enough for the tile choice to consider the 256-wide
-    float32 tiles at both register budgets (768 tiles fill one round at three
-    blocks per CU, 512 one round at two), with every operand layout pairing,
-    K tails of 8 and 4, and (last case) partial tiles in M and N."""
+@pytest.mark.parametrize("dtype,nbatch,M,N,K", [(torch.float32, 96, 512, 512, 40), (torch.float32, 64, 512, 512, 36),
+                                                (torch.float32, 48, 520, 264, 100),
+                                                (torch.float16, 96, 512, 512, 40), (torch.float16, 64, 512, 512, 72),
+                                                (torch.float16, 48, 520, 264, 104), (torch.float16, 2, 1024, 1024, 512)],
+                         ids=["f32-768t-k40", "f32-512t-k36", "f32-partial", "f16-768t-k40", "f16-512t-k72",
+                              "f16-partial", "f16-compute"])
+def test_gemm_grids_of_wide_tiles(layout_a, layout_b, dtype, nbatch, M, N, K):
+    """Grids large enough for the tile choice to consider the 256-wide tiles
+    at both register budgets (768 tiles fill one round at three blocks per
+    CU, 512 one round at two), with every operand layout pairing (float16
+    k-major operands go through the transposing LDS read), K tails inside the
+    last slab, partial tiles in M and N, and (last case) a compute-bound
+    float16 grid that runs persistent."""
     g = torch.Generator().manual_seed(nbatch + M + K)
-    A = torch.randn(nbatch, M, K, generator=g)
-    B = torch.randn(nbatch, K, N, generator=g)
+    A = torch.randn(nbatch, M, K, generator=g).to(dtype)
+    B = torch.randn(nbatch, K, N, generator=g).to(dtype)
     if layout_a == "mn":
         a_buf, a_ms, a_ks = A.transpose(1, 2).contiguous(), 1, M
     else:
@@ -193,8 +200,10 @@ def test_gemm_float32_grids_of_wide_tiles(layout_a, layout_b, nbatch, M, N, K):
         b_buf, b_ks, b_ns = B.contiguous(), N, 1
     else:
         b_buf, b_ks, b_ns = B.transpose(1, 2).contiguous(), 1, K
+    code = launch.DT_F32 if dtype == torch.float32 else launch.DT_F16
     got = _gemm_direct(a_buf.reshape(-1).cuda(), b_buf.reshape(-1).cuda(), M, N, K, a_ms, a_ks, b_ks, b_ns,
-                       launch.DT_F32, nbatch=nbatch)
+                       code, nbatch=nbatch)
     want = torch.bmm(A.double().cuda(), B.double().cuda()).cpu()
     scale = float(want.abs().max())
-    assert float((got.double() - want).abs().max()) <= 1e-4 * scale
+    rtol = 1e-4 if dtype == torch.float32 else 2e-3
+    assert float((got.double() - want).abs().max()) <= rtol * scale
