@@ -16,6 +16,10 @@ microseconds, less than one Python-level call costs, so each is captured once
 in a HIP graph and the graph is replayed between two events: the figure is the
 GPU time of the einsum's launches.
 
+``large_f16`` times 8192^3 float16 contractions (float32 output) in the
+NN and NT layouts on the dense float16 MFMA roof, with torch.matmul (the
+vendor library, float16 output) beside them.
+
 ``gdn`` times the GDN contraction set at the reference's sizes the same way,
 and ``gdn_stages`` two of its stage sequences issued eagerly (one Python call
 per launch) and replayed as one HIP graph (``pto_einsum.StageGraph``).
@@ -432,6 +436,51 @@ def roofline(flops, nbytes, t_ms, dtype):
                 frac=round(gbs / PEAK_HBM_GBS, 4)), tflops, gbs
 
 
+def time_large_f16(dev, steps, warmup):
+    """Large float16 contractions (float32 output): the north star's
+    "large fp16 contractions" on the dense float16 MFMA roof, with torch's
+    matmul (the vendor library, float16 output) timed beside them."""
+    import torch
+
+    from pto_einsum import EinsumBuilder
+
+    out = []
+    n = 8192
+    g = torch.Generator().manual_seed(77)
+    x = (torch.randn(n, n, generator=g) / 64).half().to(dev)
+    y = (torch.randn(n, n, generator=g) / 64).half().to(dev)
+    for eq, label in (("ij,jk->ik", "NN"), ("ik,jk->ij", "NT")):
+        r = EinsumBuilder(eq, [tuple(x.shape), tuple(y.shape)], torch.float16).build()
+        f, nb = work(eq, x, y)
+        km = time_graph(r, x, y, max(5, steps // 2), max(2, warmup // 2), r(x, y).numel() * 4)
+        rf, tf, gb = roofline(f, nb, km, "f16")
+        out.append(dict(shape=f"{n}^3 {label}", equation=eq, dtype="f16", us=round(km * 1e3, 1),
+                        tflops=round(tf, 1), roof=rf["bound"], frac=rf["frac"]))
+        log(f"bench: large f16 {eq} {km * 1e3:.1f} us {tf:.1f} TFLOP/s ({rf['frac'] * 100:.1f}% of fp16 MFMA)")
+        del r
+        torch.cuda.empty_cache()
+    yt = y.t().contiguous()
+    for label, fn in (("NN", lambda: torch.matmul(x, y)), ("NT", lambda: torch.matmul(x, yt.t()))):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(10):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        t = e0.elapsed_time(e1) / 10
+        tf = 2 * n ** 3 / t / 1e9
+        out.append(dict(shape=f"{n}^3 {label}", equation="torch.matmul (float16 output)", dtype="f16",
+                        us=round(t * 1e3, 1), tflops=round(tf, 1), roof="mfma",
+                        frac=round(tf / PEAK_TFLOPS["f16"], 4)))
+        log(f"bench: torch.matmul f16 {label} {t * 1e3:.1f} us {tf:.1f} TFLOP/s")
+    del x, y, yt
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(nbatch, budget_s=10.0, max_reps=30):
     """Reference CPU route on `nbatch` of config 2's 16 batches, 1 thread,
     called repeatedly for about `budget_s` seconds (median call time)."""
@@ -532,6 +581,7 @@ def main():
             f"the three einsums take {chain_us:.1f} us")
 
     transposes = [] if args.no_configs else time_transposes(dev, args.steps, args.warmup)
+    large_f16 = [] if args.no_configs else time_large_f16(dev, args.steps, args.warmup)
     gdn, gdn_stages = ([], []) if args.no_configs else time_gdn(dev, args.steps, args.warmup)
 
     log("bench: timing the CPU baseline")
@@ -557,6 +607,7 @@ def main():
         "cpu_baseline": cpu,
         "per_config": per_config,
         "transposes": transposes,
+        "large_f16": large_f16,
         "gdn": gdn,
         "gdn_stages": gdn_stages,
     }
