@@ -101,14 +101,15 @@ int gemm_occupancy_f16(int bm, int bn);
 hipError_t launch_gemm_f32(int bm, int bn, int alayout, int blayout, int persist, const GemmArgs& g,
                            hipStream_t s);
 // Direct-load kernel (pe_gemm_dl.h, float32 and float16): 64x64, 128x128,
-// 256x128 and 128x256 tiles, L_MN or L_K operands with the vector conditions
-// gemm_dl_eligible checks.  minb: register budget of the 256-wide tiles
-// (2 or 3 resident blocks per CU; 64x64 / 128x128 always use 4).
+// 256x128 and 128x256 tiles, L_MN or L_K operands with the vector and
+// output-stride conditions gemm_dl_eligible checks.  minb: register budget
+// of the 256-wide tiles (2 or 3 resident blocks per CU; 64x64 / 128x128
+// always use 4).
 // gemm_dl_resident returns the resident blocks per CU of one instantiation,
 // or 0 when the compiler spilled more than a few of its registers (never
 // launched).  persist: a grid of resident blocks walking the tiles (else one
 // block per tile).
-bool gemm_dl_eligible(int dtype, int al, int bl, int64_t M, int64_t N, int64_t K);
+bool gemm_dl_eligible(int dtype, int al, int bl, int64_t M, int64_t N, int64_t K, int64_t c_ms, int64_t c_ns);
 int gemm_dl_resident(int dtype, int bm, int bn, int minb, int al, int bl);
 hipError_t launch_gemm_dl(int dtype, int bm, int bn, int minb, int al, int bl, bool persist, const GemmArgs& g,
                           hipStream_t s);

@@ -156,7 +156,7 @@ GemmChoice choose(const pe_gemm_desc& d, bool dl = false, int al = L_MN, int bl 
         c.bm = tall ? d.tile : 128;
         c.bn = tall ? 128 : d.tile;
         c.persist = PE_GEMM_BIG_PERSIST;
-        if (dl && gemm_dl_resident(d.dtype, c.bm, c.bn, 3, al, bl) < 1) c.minb = 2;
+        if (dl && gemm_dl_resident(d.dtype, c.bm, c.bn, 3, al, bl) < 3) c.minb = 2;
         if (dl && gemm_dl_resident(d.dtype, c.bm, c.bn, c.minb, al, bl) < 1) c.bm = c.bn = 128;
     } else {
         // 64x64 unless 128x128 tiles give every CU more than two: with two
@@ -189,8 +189,10 @@ GemmChoice choose(const pe_gemm_desc& d, bool dl = false, int al = L_MN, int bl 
                 const bool no_waste = ceil_div(d.M, bbm) * bbm * ceil_div(d.N, bbn) * bbn <=
                                       ceil_div(d.M, 128) * 128 * ceil_div(d.N, 128) * 128;
                 for (int minb = 3; minb >= 2 && bt >= cus && no_waste; --minb) {
+                    // A budget whose blocks do not all fit (LDS) gives up
+                    // registers for nothing: skip it for the next one.
                     const int res = gemm_dl_resident(d.dtype, bbm, bbn, minb, al, bl);
-                    if (res < 1) continue;
+                    if (res < minb) continue;
                     const int64_t slots = cus * res;
                     const double fill = double(bt) / double(ceil_div(bt, slots) * slots);
                     if (fill >= best + 1e-9 || (fill >= best && !taken)) {
@@ -343,8 +345,13 @@ extern "C" int pe_gemm(const pe_gemm_desc* d, const void* a, const void* b, floa
     const int vec = d->dtype == PE_F32 ? 4 : 8;
     const int al = classify(d->M, d->K, d->a_ms, d->a_ks, d->a_bstride, d->nbatch, a, vec);
     const int bl = classify(d->N, d->K, d->b_ns, d->b_ks, d->b_bstride, d->nbatch, b, vec);
-    const bool dl = d->tile != 192 && gemm_dl_eligible(d->dtype, al, bl, d->M, d->N, d->K);
+    bool dl = d->tile != 192 && gemm_dl_eligible(d->dtype, al, bl, d->M, d->N, d->K, d->c_ms, d->c_ns);
     GemmChoice ch = choose(*d, dl, al, bl);
+    if (dl && gemm_dl_resident(d->dtype, ch.bm, ch.bn, ch.minb, al, bl) < 1) {
+        // the chosen direct-load instantiation spills: the staged kernel
+        dl = false;
+        ch = choose(*d, false, al, bl);
+    }
     if (ch.nsplit > 1) {
         if (!ws || ws_bytes < ch.ws_bytes) return fail(PE_ERR_WORKSPACE, "gemm: split-K workspace missing or too small");
         if (nb * d->M * d->N >= (int64_t(1) << 32))

@@ -40,20 +40,76 @@
 // before any MFMA reads it, so no value from outside the operand reaches a
 // stored sum.  Host-side conditions (see gemm_dl_eligible): L_MN operands
 // need M (resp. N) to be a whole number of 16-byte vectors, L_K operands K
-// (and so every split's k extent), and both 16-byte aligned vectors.
+// (and so every split's k extent), and both 16-byte aligned vectors; the
+// output's strides keep every element of a tile within 2^31 bytes of the
+// tile's corner (32-bit store offsets).
 #pragma once
 
 #include "pe_gemm_kernel.h"
 
 namespace pe {
 
-// Output stores as inline assembly as well: a compiler-issued store would be
-// a tracked vector-memory operation, and the compiler then waits for the
-// whole vector-memory counter (in-flight slab loads included) before
-// reusing any register the store read.
-__device__ __forceinline__ void dl_store(float* p, float v, bool nt) {
-    if (nt) asm volatile("global_store_dword %0, %1, off nt" : : "v"(p), "v"(v));
-    else asm volatile("global_store_dword %0, %1, off" : : "v"(p), "v"(v));
+// Output stores of one wave's tile, as inline assembly: a compiler-issued
+// store would be a tracked vector-memory operation, and the compiler then
+// waits for the whole vector-memory counter (in-flight slab loads included)
+// before reusing any register the store read.  Addressing: one wave-uniform
+// 64-bit base in scalar registers and a 32-bit byte offset per lane; each
+// store adds one of four uniform row offsets to its row group's lane offset
+// in the same assembly block, so one temporary register serves every store.
+// Register 4 q + s of fragment block (i, j) is row 32 i + 8 q + s (plus 4 in
+// the upper half-wave, folded into lane_off) and column 32 j (plus the
+// lane's column, also in lane_off).  cms4 / cns4: row / column strides in
+// bytes.  MASKED: only rows below rrem and columns below crem (both relative
+// to the lane's first element) are stored.  The caller passes the strides
+// and lane values through opaque moves made in the epilogue, so nothing
+// derived from them is hoisted out of the tile loop to hold registers through
+// the MFMA loop.
+template <bool NT, bool MASKED, int FM, int FN>
+__device__ __forceinline__ void dl_store_tile(const float* wbase, uint32_t lane_off, uint32_t cms4, uint32_t cns4,
+                                              int rrem, int crem, const f32x16 (&acc)[FM][FN]) {
+    uint32_t rs[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) rs[r] = uint32_t(r) * cms4;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            if (MASKED && 32 * j >= crem) continue;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint32_t bq = lane_off + uint32_t(32 * i + 8 * q) * cms4 + uint32_t(32 * j) * cns4;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    if (MASKED && 32 * i + 8 * q + r >= rrem) continue;
+                    uint32_t t;
+                    if (NT)
+                        asm volatile("v_add_u32 %0, %1, %2\n\tglobal_store_dword %0, %3, %4 nt"
+                                     : "=&v"(t)
+                                     : "s"(rs[r]), "v"(bq), "v"(acc[i][j][4 * q + r]), "s"(wbase));
+                    else
+                        asm volatile("v_add_u32 %0, %1, %2\n\tglobal_store_dword %0, %3, %4"
+                                     : "=&v"(t)
+                                     : "s"(rs[r]), "v"(bq), "v"(acc[i][j][4 * q + r]), "s"(wbase));
+                }
+            }
+        }
+}
+
+// A wave-uniform 64-bit address moved to scalar registers for use as the
+// scalar base of vector-memory instructions.  The moves are the compiler's
+// readfirstlane (it keeps the wait state a readfirstlane needs after the
+// vector instruction that wrote its source); each half is widened as
+// unsigned (readfirstlane returns int, and a sign-extended low half would
+// corrupt the high half).  A vector instruction writing a scalar register
+// that a vector-memory instruction then reads needs five wait states: the
+// s_nop, which the stores depend on through the base.
+__device__ __forceinline__ const float* dl_uniform_base(const float* p) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = uint32_t(__builtin_amdgcn_readfirstlane(uint32_t(v)));
+    const uint32_t hi = uint32_t(__builtin_amdgcn_readfirstlane(uint32_t(v >> 32)));
+    const float* b = reinterpret_cast<const float*>((uint64_t(hi) << 32) | uint64_t(lo));
+    asm volatile("s_nop 4" : "+s"(b));
+    return b;
 }
 
 // 16 bytes per lane from global memory into LDS at lds + 16 * lane.  Written
@@ -66,7 +122,8 @@ __device__ __forceinline__ void dma16(const float* gptr, const float* lds) {
     // The LDS address is wave-uniform (M0 takes a scalar register).
     const uint32_t l = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(
         reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) float*)(lds))));
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(gptr), "s"(l) : "memory", "m0");
+    // One wait state between writing M0 and the load that reads it.
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(gptr), "s"(l) : "memory", "m0");
 }
 
 // Per-type slab geometry and MFMA.
@@ -337,24 +394,34 @@ __global__ __launch_bounds__(kGemmThreads, MINB) void gemm_dl_kernel(GemmArgs g)
             cms = g.c_ms;
             cns = g.c_ns;
         }
+        // The store assembly reads accumulators the MFMAs just wrote, a read
+        // the compiler cannot see: keep every MFMA above this point and
+        // leave the wait states an MFMA result needs before a vector-memory
+        // instruction reads it (at most 20 on this target).
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7");
         // 32x32 accumulator layout: lane l, register r holds row
         // 8*(r/4) + 4*(l/32) + r%4 and column l%32 of its block.
+        const int wm0 = ct.m0 + wm * WM, wn0 = ct.n0 + wn * WN;
+        const float* wbase = dl_uniform_base(C + int64_t(wm0) * cms + int64_t(wn0) * cns);
+        uint32_t cms4 = uint32_t(cms) * 4u, cns4 = uint32_t(cns) * 4u, ln = uint32_t(lane);
+        int rrem = g.M - wm0, crem = g.N - wn0;
+        asm volatile("" : "+s"(cms4), "+s"(cns4), "+v"(ln), "+s"(rrem), "+s"(crem));
+        const uint32_t lo = (ln >> 5) * 4u * cms4 + (ln & 31u) * cns4;
+        if (ct.m0 + BM <= g.M && ct.n0 + BN <= g.N) {
+            if (nt) dl_store_tile<true, false>(wbase, lo, cms4, cns4, 0, 0, acc);
+            else dl_store_tile<false, false>(wbase, lo, cms4, cns4, 0, 0, acc);
+        } else {
+            const int rr = rrem - 4 * int(ln >> 5), cr = crem - int(ln & 31u);
+            if (nt) dl_store_tile<true, true>(wbase, lo, cms4, cns4, rr, cr, acc);
+            else dl_store_tile<false, true>(wbase, lo, cms4, cns4, rr, cr, acc);
+        }
 #pragma unroll
-        for (int i = 0; i < FM; ++i) {
+        for (int i = 0; i < FM; ++i)
 #pragma unroll
-            for (int j = 0; j < FN; ++j) {
-                const int n = ct.n0 + wn * WN + j * 32 + (lane & 31);
-                if (n < g.N) {
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int m = ct.m0 + wm * WM + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-                        if (m < g.M) dl_store(C + int64_t(m) * cms + int64_t(n) * cns, acc[i][j][r], nt);
-                    }
-                }
+            for (int j = 0; j < FN; ++j)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-            }
-        }
     };
 
     // One slab: wait for its loads, start the next slab's loads into the

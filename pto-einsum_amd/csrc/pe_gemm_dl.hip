@@ -34,9 +34,10 @@ static int dl_index(int dtype, int bm, int bn, int minb, int al, int bl) {
 }
 
 // Instantiations whose register allocation spilled more than this many bytes
-// per lane are never launched.  The 128x256 tile at three blocks per CU
-// spills one lane offset (8 bytes, reloaded once per slab) and runs config 2
-// as fast as the spill-free variants; larger spills sit inside the MFMA loop.
+// per lane are never launched (larger spills sit inside the MFMA loop).  Of
+// the 256-wide tiles at three blocks per CU, those with one or both operands
+// k-contiguous spill 8-12 bytes (a lane offset reloaded once per slab) and
+// run as fast as spill-free ones; the float16 ones spill hundreds.
 #ifndef PE_GEMM_DL_MAX_SPILL
 #define PE_GEMM_DL_MAX_SPILL 16
 #endif
@@ -61,7 +62,7 @@ int gemm_dl_resident(int dtype, int bm, int bn, int minb, int al, int bl) {
     return c;
 }
 
-bool gemm_dl_eligible(int dtype, int al, int bl, int64_t M, int64_t N, int64_t K) {
+bool gemm_dl_eligible(int dtype, int al, int bl, int64_t M, int64_t N, int64_t K, int64_t c_ms, int64_t c_ns) {
     if (!PE_GEMM_DL) return false;
     if (dtype == PE_F16 && !PE_GEMM_DL_F16) return false;
     const int vec = dtype == PE_F32 ? 4 : 8;  // elements per 16-byte vector
@@ -70,6 +71,11 @@ bool gemm_dl_eligible(int dtype, int al, int bl, int64_t M, int64_t N, int64_t K
     if (al == L_MN && M % vec != 0) return false;
     if (bl == L_MN && N % vec != 0) return false;
     if ((al == L_K || bl == L_K) && K % vec != 0) return false;
+    // 32-bit store offsets: every element of a tile (at most 256 x 256)
+    // within 2^31 bytes of its corner, for the output and for the row-major
+    // split-K partials (strides N and 1).
+    const int64_t lim = int64_t(1) << 29;
+    if (c_ms < 0 || c_ns < 0 || 255 * (c_ms + c_ns) >= lim || 255 * (N + 1) >= lim) return false;
     return true;
 }
 

@@ -162,6 +162,39 @@ def test_gemm_tiles_direct(tile, dtype, M, N, K, layout, split_k):
     assert float(np.abs(got.numpy() - want).max()) <= rtol * scale
 
 
+@pytest.mark.parametrize("c_ms", [2_000_003, 2_200_001], ids=["dl-near-limit", "staged-beyond-limit"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16], ids=["f32", "f16"])
+def test_gemm_large_output_row_stride(c_ms, dtype):
+    """Output rows ~8 MB apart: just under the direct-load kernel's limit
+    (every element of a 256 x 256 tile within 2^31 bytes of its corner, so
+    in-tile store offsets reach ~500 MB) and just over it (the staged kernel
+    takes the call), with partial tiles in M and N."""
+    M, N, K = 130, 70, 40
+    g = torch.Generator().manual_seed(c_ms % 1000)
+    A = torch.randn(M, K, generator=g).to(dtype)
+    B = torch.randn(K, N, generator=g).to(dtype)
+    lib = abi.bind()
+    c_numel = (M - 1) * c_ms + N
+    code = launch.DT_F32 if dtype == torch.float32 else launch.DT_F16
+    d = launch.GemmDesc(dtype=code, batch_shape=[1], a_bstride=[M * K], b_bstride=[K * N], c_bstride=[c_numel],
+                        M=M, N=N, K=K, a_ms=K, a_ks=1, b_ks=N, b_ns=1, c_ms=c_ms, c_ns=1, a_numel=M * K,
+                        b_numel=K * N, c_numel=c_numel)
+    cd = abi.gemm_desc(d)
+    ws_bytes = lib.pe_gemm_workspace_bytes(ctypes.byref(cd))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device="cuda")
+    c = torch.full((c_numel,), float("nan"), dtype=torch.float32, device="cuda")
+    a, b = A.contiguous().cuda(), B.contiguous().cuda()
+    rc = lib.pe_gemm(ctypes.byref(cd), _ptr(a), _ptr(b), ctypes.c_void_p(c.data_ptr()), _ptr(ws), ws_bytes,
+                     _stream())
+    assert rc == 0, runtime.last_error()
+    got = torch.as_strided(c, (M, N), (c_ms, 1)).cpu().double()
+    gaps = torch.as_strided(c, (M - 1, 16), (c_ms, 1), N).cpu()
+    want = A.double() @ B.double()
+    rtol = 1e-4 if dtype == torch.float32 else 2e-3
+    assert float((got - want).abs().max()) <= rtol * float(want.abs().max())
+    assert bool(torch.isnan(gaps).all())  # nothing stored between the rows
+
+
 def test_gemm_rejects_bad_tile():
     lib = abi.bind()
     d = launch.GemmDesc(dtype=launch.DT_F16, batch_shape=[1], a_bstride=[0], b_bstride=[0], c_bstride=[0],
