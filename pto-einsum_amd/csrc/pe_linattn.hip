@@ -10,8 +10,8 @@
 // keeps each 32x32 block of A in registers:
 //
 //   1. S^T block = K_blk . Q_blk^T on MFMA (v_mfma_f32_32x32x16_f16 for float16
-//      q/k, v_mfma_f32_32x32x2_f32 for float32), float32 accumulation in two
-//      chains (even / odd k steps) added at the end.  With K as the A operand,
+//      q/k, v_mfma_f32_32x32x2_f32 for float32), float32 accumulation (float32:
+//      in two chains, even / odd k steps, added at the end).  With K as the A operand,
 //      lane l ends up holding row t = l%32 of the block and the 16 values
 //      s = 8*(r/4) + 4*(l/32) + r%4, r = 0..15.
 //   2. Those 16 values are multiplied by the mask in registers (one float32
@@ -68,14 +68,19 @@ struct VTileSplit {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-// Round-to-nearest-even split of a float32 into two bfloat16 terms: x = hi +
+// Round-to-nearest-even split of two float32 into bfloat16 terms: x = hi +
 // lo + e with |e| <= 2^-16 |x| (hi carries the top 8 significant bits, lo the
-// next 8; x - hi is exact in float32).
-__device__ __forceinline__ void split_bf16(float x, __bf16& hi, __bf16& lo) {
-    hi = __bf16(x);
-    lo = __bf16(x - float(hi));
+// next 8; x - hi is exact in float32).  hi and lo come back packed, x0's term
+// in the low half: each pair conversion is one v_cvt_pk_bf16_f32.
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void split_bf16x2(float x0, float x1, uint32_t& hi, uint32_t& lo) {
+    const f32x2_t x = {x0, x1};
+    hi = __builtin_bit_cast(uint32_t, __builtin_convertvector(x, bf16x2_t));
+    const float h0 = __builtin_bit_cast(float, hi << 16), h1 = __builtin_bit_cast(float, hi & 0xffff0000u);
+    const f32x2_t r = {x0 - h0, x1 - h1};
+    lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(r, bf16x2_t));
 }
-__device__ __forceinline__ uint16_t bf16_bits(__bf16 x) { return __builtin_bit_cast(uint16_t, x); }
 
 struct LinAttnArgs {
     const void* q;
@@ -243,14 +248,13 @@ __global__ __launch_bounds__(256, 2) void linattn_kernel(LinAttnArgs a) {
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh) {
                 u32x4 wh, wl;
+                uint32_t h4[4], l4[4];
 #pragma unroll
-                for (int j = 0; j < 8; j += 2) {
-                    __bf16 h0, l0, h1, l1;
-                    split_bf16(val(8 * (j / 4) + 4 * hh + j % 4), h0, l0);
-                    split_bf16(val(8 * ((j + 1) / 4) + 4 * hh + (j + 1) % 4), h1, l1);
-                    wh[j / 2] = uint32_t(bf16_bits(h0)) | (uint32_t(bf16_bits(h1)) << 16);
-                    wl[j / 2] = uint32_t(bf16_bits(l0)) | (uint32_t(bf16_bits(l1)) << 16);
-                }
+                for (int j = 0; j < 8; j += 2)
+                    split_bf16x2(val(8 * (j / 4) + 4 * hh + j % 4), val(8 * ((j + 1) / 4) + 4 * hh + (j + 1) % 4),
+                                 h4[j / 2], l4[j / 2]);
+                wh = u32x4{h4[0], h4[1], h4[2], h4[3]};
+                wl = u32x4{l4[0], l4[1], l4[2], l4[3]};
                 *reinterpret_cast<u32x4*>(&vt[st].hi[vp][vs0 + 8 * hh]) = wh;
                 *reinterpret_cast<u32x4*>(&vt[st].lo[vp][vs0 + 8 * hh]) = wl;
             }
@@ -296,27 +300,30 @@ __global__ __launch_bounds__(256, 2) void linattn_kernel(LinAttnArgs a) {
         __syncthreads();
         if (sb + kSB < s_end) prefetch(sb + kSB);
 
-        bool nz = false;
+        // Any mask value other than +-0 (or of the bits, sign dropped).
+        uint32_t mbits = 0;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) nz = nz || (mv[r] != 0.0f);
-        if (__any(nz)) {
-            // 1. S^T block: rows s (this lane: 16 of them), column t = l32, in
-            //    two accumulation chains (even / odd k steps).
+        for (int r = 0; r < 16; ++r) mbits |= __builtin_bit_cast(uint32_t, mv[r]);
+        if (__any((mbits << 1) != 0u)) {
+            // 1. S^T block: rows s (this lane: 16 of them), column t = l32.
+            //    float16: one accumulation chain (dependent 32x32 MFMAs issue
+            //    back to back); float32 (64 k steps): two, even / odd.
             const T* krow = &kt[stage][l32 * KT::PITCH + noff];
-            f32x16 sacc[2];
+            constexpr int NCH = QK::kBytes == 2 ? 1 : 2;
+            f32x16 sacc[NCH];
 #pragma unroll
-            for (int c = 0; c < 2; ++c)
+            for (int c = 0; c < NCH; ++c)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) sacc[c][r] = 0.0f;
 #pragma unroll
             for (int kk = 0; kk < NSTEPS; ++kk) {
                 const typename F::type kf = *reinterpret_cast<const typename F::type*>(krow + kk * F::KSTEP);
-                sacc[kk & 1] = F::mfma(kf, qf[kk], sacc[kk & 1]);
+                sacc[kk % NCH] = F::mfma(kf, qf[kk], sacc[kk % NCH]);
             }
             // 2. Mask product (float32, one rounding).
             float av[16];
 #pragma unroll
-            for (int r = 0; r < 16; ++r) av[r] = (sacc[0][r] + sacc[1][r]) * mv[r];
+            for (int r = 0; r < 16; ++r) av[r] = (NCH == 1 ? sacc[0][r] : sacc[0][r] + sacc[NCH - 1][r]) * mv[r];
             // 3. out[t, p] += sum_s A[t, s] v[s, p].  The four 32-column blocks
             //    are interleaved: four independent chains.
             if constexpr (PV32) {
@@ -342,14 +349,11 @@ __global__ __launch_bounds__(256, 2) void linattn_kernel(LinAttnArgs a) {
                 // below 2^-16 |P||V|).
 #pragma unroll
                 for (int q2 = 0; q2 < 2; ++q2) {
-                    bf16x8 ph, pl;
+                    uint32_t h4[4], l4[4];
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        __bf16 x, y;
-                        split_bf16(av[8 * q2 + j], x, y);
-                        ph[j] = x;
-                        pl[j] = y;
-                    }
+                    for (int j = 0; j < 8; j += 2) split_bf16x2(av[8 * q2 + j], av[8 * q2 + j + 1], h4[j / 2], l4[j / 2]);
+                    const u32x4 phw = {h4[0], h4[1], h4[2], h4[3]}, plw = {l4[0], l4[1], l4[2], l4[3]};
+                    const bf16x8 ph = __builtin_bit_cast(bf16x8, phw), pl = __builtin_bit_cast(bf16x8, plw);
 #pragma unroll
                     for (int jb = 0; jb < 4; ++jb) {
                         const bf16x8 vh = *reinterpret_cast<const bf16x8*>(&vt[stage].hi[32 * jb + l32][16 * q2 + 8 * h]);
