@@ -39,9 +39,12 @@ namespace pe {
 
 // Deterministic split reduction.  Each thread owns VEC consecutive outputs
 // and sums their nsplit partials in ascending split order, from +0, exactly
-// as a sequential loop would; the partial loads are issued eight splits at a
-// time so their latencies overlap instead of adding up.
-template <int VEC>
+// as a sequential loop would; the partial loads are issued U splits at a time
+// so their latencies overlap instead of adding up (U = 16 covers the 16
+// splits of the fused chain in one round).  VST: the VEC outputs are
+// consecutive elements of one output row, 16-byte aligned, stored as one
+// vector.
+template <int VEC, int U, bool VST>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(ReduceArgs r) {
     using V = typename Pack<VEC, float>::type;
     const uint32_t nv = r.per_split / VEC;
@@ -50,15 +53,15 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(ReduceArgs r) {
         float acc[VEC];
 #pragma unroll
         for (int e = 0; e < VEC; ++e) acc[e] = 0.0f;
-        for (int s0 = 0; s0 < r.nsplit; s0 += 8) {
-            V x[8];
+        for (int s0 = 0; s0 < r.nsplit; s0 += U) {
+            V x[U];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
+            for (int u = 0; u < U; ++u) {
                 const int sp = min(s0 + u, r.nsplit - 1);
                 x[u] = *reinterpret_cast<const V*>(r.partial + int64_t(sp) * r.per_split + int64_t(i) * VEC);
             }
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
+            for (int u = 0; u < U; ++u) {
                 if (s0 + u < r.nsplit) {
                     if constexpr (VEC == 1) {
                         acc[0] = acc[0] + x[u];
@@ -69,9 +72,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(ReduceArgs r) {
                 }
             }
         }
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-            const uint32_t idx = i * VEC + e;
+        auto offset = [&](uint32_t idx) {
             uint32_t rest, n, batch, m;
             r.n_div.divmod(idx, rest, n);
             r.m_div.divmod(rest, batch, m);
@@ -82,20 +83,34 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(ReduceArgs r) {
                 off += int64_t(rr) * r.c_bs[d];
                 batch = q;
             }
-            store_f(r.c + off, acc[e], r.store_nt != 0);
+            return off;
+        };
+        if constexpr (VST) {
+            const f32x4 v = {acc[0], acc[1], acc[2], acc[3]};
+            store_f(reinterpret_cast<f32x4*>(r.c + offset(i * VEC)), v, r.store_nt != 0);
+        } else {
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) store_f(r.c + offset(i * VEC + e), acc[e], r.store_nt != 0);
         }
     }
 }
 
 hipError_t launch_splitk_reduce(const ReduceArgs& r, hipStream_t s) {
     const bool vec = r.per_split % 4 == 0 && (r.nsplit == 0 || aligned(r.partial, 16));
+    // Four consecutive outputs form one aligned vector of one output row.
+    bool vst = vec && r.c_ns == 1 && r.n_div.d % 4 == 0 && r.c_ms % 4 == 0 && aligned(r.c, 16);
+    for (int d = 0; d < r.nbatch; ++d) vst = vst && r.c_bs[d] % 4 == 0;
     const int64_t items = vec ? r.per_split / 4 : r.per_split;
     const int grid = int(std::max<int64_t>(1, std::min<int64_t>(ceil_div(items, 256), cu_count() * 8)));
-    if (vec)
-        hipLaunchKernelGGL(splitk_reduce_kernel<4>, dim3(grid), dim3(256), 0, s, r);
-    else
-        hipLaunchKernelGGL(splitk_reduce_kernel<1>, dim3(grid), dim3(256), 0, s, r);
-    return hipGetLastError();
+    const bool wide = r.nsplit > 8;
+    const void* k = vst ? (wide ? reinterpret_cast<const void*>(&splitk_reduce_kernel<4, 16, true>)
+                                : reinterpret_cast<const void*>(&splitk_reduce_kernel<4, 8, true>))
+                  : vec ? (wide ? reinterpret_cast<const void*>(&splitk_reduce_kernel<4, 16, false>)
+                                : reinterpret_cast<const void*>(&splitk_reduce_kernel<4, 8, false>))
+                        : reinterpret_cast<const void*>(&splitk_reduce_kernel<1, 8, false>);
+    ReduceArgs a = r;
+    void* args[] = {&a};
+    return hipLaunchKernel(k, dim3(grid), dim3(256), args, 0, s);
 }
 
 namespace {
