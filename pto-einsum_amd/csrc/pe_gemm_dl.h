@@ -47,6 +47,7 @@
 
 #include "pe_gemm_kernel.h"
 
+
 namespace pe {
 
 // Output stores of one wave's tile, as inline assembly: a compiler-issued
@@ -438,6 +439,10 @@ __global__ __launch_bounds__(kGemmThreads, MINB) void gemm_dl_kernel(GemmArgs g)
             asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         }
         typename M::Frag fa[FM][OA::RING], fb[FN][OB::RING];
+        // Raised wave priority for the slab's fragment reads and MFMAs: the
+        // SIMD then issues this wave's MFMAs ahead of other waves' loads and
+        // address work (4096^3 float32 -3 %, 8192^3 float16 -1.5 % on one box).
+        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int i = 0; i < FM; ++i) OA::frag(sa, loa, wm * WM, i, 0, fa[i]);
 #pragma unroll
@@ -460,6 +465,7 @@ __global__ __launch_bounds__(kGemmThreads, MINB) void gemm_dl_kernel(GemmArgs g)
                 for (int j = 0; j < FN; ++j)
                     acc[i][j] = M::mfma(fa[i][st % OA::RING], fb[j][st % OB::RING], acc[i][j]);
         }
+        __builtin_amdgcn_s_setprio(0);
         if (++cs == ct.nslabs) {
             epilogue();
             cbid += walk.step;
