@@ -147,6 +147,27 @@ int64_t pe_linear_attention_workspace_bytes(const pe_linattn_desc* d);
 int pe_linear_attention(const pe_linattn_desc* d, const void* q, const void* k, const void* v,
                         const void* m, float* out, void* ws, int64_t ws_bytes, void* stream);
 
+/* Sum over the solo axes of one einsum operand (an index found in that
+ * operand only and not in the output).  No entry point of the reference
+ * corresponds: it rejects such equations (builder.py:218-229); this is the
+ * reduction stage its roadmap describes for them (IMPLEMENTATION.md:812-821,
+ * "Option A"), reached from Python through einsum(..., reduce_solo_axes=True).
+ *   dst[k] = sum over r of (float)src[sum_d k_d keep_stride[d] + sum_e r_e red_stride[e]]
+ * with k the row-major index over keep_shape (dst contiguous float32) and r
+ * over red_shape.  Each output sums its terms in row-major order of r from +0,
+ * as a sequential loop (deterministic).  nred = 0 is a conversion to float32. */
+typedef struct pe_reduce_desc {
+    int32_t dtype;                      /* PE_F32 or PE_F16 */
+    int32_t nkeep;                      /* 0..PE_MAX_DIMS */
+    int32_t nred;                       /* 0..PE_MAX_DIMS */
+    int32_t reserved;                   /* must be 0 */
+    int64_t keep_shape[PE_MAX_DIMS], keep_stride[PE_MAX_DIMS];
+    int64_t red_shape[PE_MAX_DIMS], red_stride[PE_MAX_DIMS];
+    int64_t src_numel;
+} pe_reduce_desc;
+
+int pe_reduce_axes(const pe_reduce_desc* d, const void* src, float* dst, void* stream);
+
 /* Plan executor: the body of every per-shape run_einsum_exec. */
 int pe_einsum_exec(const pe_einsum_plan* p, const void* in0, const void* in1, float* out,
                    void* ws, void* stream);

@@ -8,6 +8,9 @@ Public API, unchanged from the reference (src/pto_einsum/__init__.py:12-15):
 
 Beyond the reference's surface:
 
+    einsum(eq, a, b, reduce_solo_axes=True) -> also sums indices found in one operand
+                                               only (e.g. "ij,jk->k"), which the
+                                               reference rejects
     linear_attention(q, k, v, m)            -> fused einsum("tn,sn,sp,ts->tp"), float32
     StageGraph(fn)                          -> fn's launches captured into one HIP graph
 

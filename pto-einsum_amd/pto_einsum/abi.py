@@ -1,8 +1,8 @@
 """ctypes mirrors of the core library's C structs (include/pto_einsum_hip.h).
 
 Lets Python callers (and the component tests) drive the core launchers
-directly: ``pe_product``, ``pe_permute``, ``pe_gemm``, ``pe_linear_attention``
-and the plan executor.
+directly: ``pe_product``, ``pe_permute``, ``pe_gemm``, ``pe_linear_attention``,
+``pe_reduce_axes`` and the plan executor.
 """
 from __future__ import annotations
 
@@ -58,6 +58,13 @@ class LinAttnDesc(ctypes.Structure):
                 ("m_numel", ctypes.c_int64), ("precise", ctypes.c_int32), ("reserved", ctypes.c_int32)]
 
 
+class ReduceDesc(ctypes.Structure):
+    _fields_ = [("dtype", ctypes.c_int32), ("nkeep", ctypes.c_int32), ("nred", ctypes.c_int32),
+                ("reserved", ctypes.c_int32),
+                ("keep_shape", _I64x8), ("keep_stride", _I64x8), ("red_shape", _I64x8), ("red_stride", _I64x8),
+                ("src_numel", ctypes.c_int64)]
+
+
 def _set(arr, values: Sequence[int]):
     for i, v in enumerate(values):
         arr[i] = int(v)
@@ -110,7 +117,8 @@ def bind(lib=None):
     lib.pe_linear_attention.argtypes = [ctypes.POINTER(LinAttnDesc), vp, vp, vp, vp, vp, vp, ctypes.c_int64, vp]
     lib.pe_linear_attention_workspace_bytes.argtypes = [ctypes.POINTER(LinAttnDesc)]
     lib.pe_linear_attention_workspace_bytes.restype = ctypes.c_int64
+    lib.pe_reduce_axes.argtypes = [ctypes.POINTER(ReduceDesc), vp, vp, vp]
     for f in ("pe_product", "pe_permute", "pe_gemm", "pe_einsum_exec", "pe_einsum_teardown", "pe_einsum_run",
-              "pe_linear_attention"):
+              "pe_linear_attention", "pe_reduce_axes"):
         getattr(lib, f).restype = ctypes.c_int
     return lib

@@ -240,18 +240,71 @@ _runners: "collections.OrderedDict" = collections.OrderedDict()
 _runners_lock = threading.Lock()
 
 
-def einsum(equation: str, *operands, device: str = "cuda"):
+def _reduce_operand(x: torch.Tensor, subs: str, solo: str) -> torch.Tensor:
+    """Sum x over the axes named in `solo` (pe_reduce_axes): a contiguous
+    float32 tensor over the other axes, in their order in `subs`.  With no
+    solo axis, x converted to float32."""
+    from . import abi
+
+    keep = [i for i, a in enumerate(subs) if a not in solo]
+    red = [i for i, a in enumerate(subs) if a in solo]
+    d = abi.ReduceDesc()
+    d.dtype = 1 if x.dtype == torch.float16 else 0
+    d.nkeep, d.nred, d.reserved = len(keep), len(red), 0
+    for j, i in enumerate(keep):
+        d.keep_shape[j], d.keep_stride[j] = x.shape[i], x.stride(i)
+    for j, i in enumerate(red):
+        d.red_shape[j], d.red_stride[j] = x.shape[i], x.stride(i)
+    d.src_numel = x.untyped_storage().nbytes() // x.element_size() - x.storage_offset()
+    out = torch.empty([x.shape[i] for i in keep], dtype=torch.float32, device=x.device)
+    lib = abi.bind()
+    with torch.cuda.device(x.device):
+        stream = ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream)
+        rc = lib.pe_reduce_axes(ctypes.byref(d), ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(out.data_ptr()), stream)
+    runtime.check(rc, "pe_reduce_axes")
+    return out
+
+
+def _reduce_solo_axes(equation: str, inp0: torch.Tensor, inp1: torch.Tensor):
+    """Sums every single-operand reduction axis (an index in one operand only
+    and not in the output, e.g. i in ``ij,jk->k``) out of its operand, as
+    torch.einsum does, and returns the remaining two-operand equation with
+    its operands.  The reference rejects such equations (builder.py:218-229);
+    this is the reduction stage its roadmap describes (IMPLEMENTATION.md:
+    812-821).  The reduced operand is float32; a float16 partner is converted
+    to float32 too, since both operands of the contraction share a dtype."""
+    reduced, in0, in1, solo0, solo1 = planner.solo_split(equation, inp0.shape, inp1.shape)
+    if not solo0 and not solo1:
+        return equation, inp0, inp1
+    if not (inp0.is_cuda and inp1.is_cuda):
+        raise ValueError("einsum: reduce_solo_axes needs both operands on the GPU")
+    if inp0.dtype not in (torch.float32, torch.float16):
+        raise TypeError(f"Unsupported torch dtype {inp0.dtype}")
+    r0 = _reduce_operand(inp0, in0, solo0) if solo0 or inp0.dtype != torch.float32 else inp0
+    r1 = _reduce_operand(inp1, in1, solo1) if solo1 or inp1.dtype != torch.float32 else inp1
+    return reduced, r0, r1
+
+
+def einsum(equation: str, *operands, device: str = "cuda", reduce_solo_axes: bool = False):
     """One-shot einsum of two operands; returns a float32 tensor.
 
     Reference: builder.py:887-902.  Runners are cached in-process by
     (equation, shapes, dtype, device), so a repeated call reuses the loaded
     library and workspace instead of re-planning and re-loading.
+
+    ``reduce_solo_axes`` (keyword only, off by default, no counterpart in the
+    reference): an index found in one operand only and not in the output is
+    summed out of that operand on the GPU first, as torch.einsum does
+    (e.g. ``ij,jk->k``); the result is computed in float32.  Off, such
+    equations raise the reference's ValueError.
     """
     if len(operands) != 2:
         raise ValueError("Only exactly two operands are supported.")
     inp0, inp1 = operands
     if inp0.dtype != inp1.dtype:
         raise ValueError("Operands must have the same datatype.")
+    if reduce_solo_axes:
+        equation, inp0, inp1 = _reduce_solo_axes(equation, inp0, inp1)
     key = (equation, tuple(inp0.shape), tuple(inp1.shape), inp0.dtype, _normalise_device(device),
            os.getenv("EINSUM_BUILD_DIR", ""), os.getenv("EINSUM_EXTRA_DEFINES", ""))
     with _runners_lock:

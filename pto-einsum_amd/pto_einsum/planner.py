@@ -99,6 +99,23 @@ def validate_expr(fn: str, shape0: Sequence[int], shape1: Sequence[int]):
     return f"{in0},{in1}->{out}", out_shape
 
 
+def solo_split(fn: str, shape0: Sequence[int], shape1: Sequence[int]):
+    """Single-operand reduction axes of a validated equation: the indices of
+    each input found in neither the other input nor the output (torch sums
+    them; the reference rejects them, builder.py:218-229).  Returns
+    ``(reduced_equation, in0, in1, solo0, solo1)``: the equation with those
+    indices removed, the two input subscripts and the solo indices of each
+    input in subscript order.  Summing them out of their operands first and
+    contracting the rest gives the same sum."""
+    norm, _ = validate_expr(fn, shape0, shape1)
+    in0, in1, out = split_equation(norm)
+    solo0 = "".join(a for a in in0 if a not in in1 and a not in out)
+    solo1 = "".join(a for a in in1 if a not in in0 and a not in out)
+    e0 = "".join(a for a in in0 if a not in solo0)
+    e1 = "".join(a for a in in1 if a not in solo1)
+    return f"{e0},{e1}->{out}", in0, in1, solo0, solo1
+
+
 def _tile_size() -> int:
     return int(os.getenv("EINSUM_TILE_SIZE", "128"))
 

@@ -92,6 +92,8 @@ int main() {
   OFF(pe_linattn_desc, m_numel); OFF(pe_linattn_desc, precise);
   OFF(pe_product_desc, b_numel); OFF(pe_permute_desc, src_numel); OFF(pe_gemm_desc, M);
   OFF(pe_gemm_desc, c_numel); OFF(pe_einsum_plan, gemm); OFF(pe_einsum_plan, ws_bytes);
+  printf("pe_reduce_desc %zu\n", sizeof(pe_reduce_desc));
+  OFF(pe_reduce_desc, red_stride); OFF(pe_reduce_desc, src_numel);
   return 0;
 }
 """
@@ -117,6 +119,9 @@ def test_ctypes_struct_layout_matches_c(tmp_path):
     assert int(vals["pe_linattn_desc"]) == ctypes.sizeof(abi.LinAttnDesc)
     assert int(vals["pe_linattn_desc.m_numel"]) == abi.LinAttnDesc.m_numel.offset
     assert int(vals["pe_linattn_desc.precise"]) == abi.LinAttnDesc.precise.offset
+    assert int(vals["pe_reduce_desc"]) == ctypes.sizeof(abi.ReduceDesc)
+    assert int(vals["pe_reduce_desc.red_stride"]) == abi.ReduceDesc.red_stride.offset
+    assert int(vals["pe_reduce_desc.src_numel"]) == abi.ReduceDesc.src_numel.offset
 
 
 def test_descriptor_validation_rejects_out_of_bounds():
