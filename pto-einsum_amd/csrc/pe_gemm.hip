@@ -159,6 +159,7 @@ bool wide_along_m(const pe_gemm_desc& d) {
 // that need no split).
 GemmChoice choose(const pe_gemm_desc& d, bool dl = false, int al = L_MN, int bl = L_MN) {
     GemmChoice c{};
+    int64_t long_k_split = 0;
     c.minb = 3;
     c.nbatch_total = batch_total(d);
     const int bk = gemm_bk(d.dtype);
@@ -179,8 +180,20 @@ GemmChoice choose(const pe_gemm_desc& d, bool dl = false, int al = L_MN, int bl 
         // load latency than their lower MFMA density costs (measured on
         // MI355X for batched 128^3 blocks and 2048^2 outputs at K = 128..512).
         c.bm = (d.M > 64 && d.N > 64) ? 128 : 64;
-        if (c.bm == 128 && c.nbatch_total * ceil_div(d.M, 128) * ceil_div(d.N, 128) <= PE_GEMM_SMALL_TILE_CUS * cus)
-            c.bm = 64;
+        const int64_t tiles128 = c.nbatch_total * ceil_div(d.M, 128) * ceil_div(d.N, 128);
+        if (c.bm == 128 && tiles128 <= PE_GEMM_SMALL_TILE_CUS * cus) c.bm = 64;
+        // Long-K grids that need a K split with either tile: 128x128 tiles
+        // split to about two blocks per CU, each split at least 16 slabs
+        // deep, beat 64x64 tiles (config 5.3, ts,sp->tp float32 with K = 4096:
+        // 52.5 us against 57.1 us on one MI355X).
+        if (d.M > 64 && d.N > 64 && tiles128 < cus && d.split_k == 0 &&
+            c.nbatch_total * d.M * d.N < (int64_t(1) << 32)) {
+            const int64_t s2 = std::min<int64_t>(32, ceil_div(2 * cus, tiles128));
+            if (d.K >= 16 * bk * s2) {
+                c.bm = 128;
+                long_k_split = s2;
+            }
+        }
         c.bn = c.bm;
         if (PE_GEMM_BIG && dl && c.bm == 128 && !hbm_bound(d)) {
             // Direct-load 256x128 / 128x256 tiles come in two register
@@ -251,6 +264,8 @@ GemmChoice choose(const pe_gemm_desc& d, bool dl = false, int al = L_MN, int bl 
     int64_t split = 1;
     if (d.split_k > 0) {
         split = d.split_k;
+    } else if (long_k_split > 0) {
+        split = long_k_split;
     } else if (tiles < cus && c.nbatch_total * d.M * d.N < (int64_t(1) << 32)) {
         // Fill about four blocks per CU, keeping at least four K slabs per split.
         split = std::min<int64_t>(ceil_div(4 * cus, tiles), std::max<int64_t>(1, d.K / (4 * bk)));

@@ -195,6 +195,24 @@ def test_gemm_large_output_row_stride(c_ms, dtype):
     assert bool(torch.isnan(gaps).all())  # nothing stored between the rows
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16], ids=["f32", "f16"])
+@pytest.mark.parametrize("M,K,N", [(4096, 4096, 128), (1024, 8192, 1024), (1000, 6000, 300)])
+def test_long_k_split_grids(dtype, M, K, N):
+    """Long-K products that the tile choice runs as 128x128 tiles split over
+    K at about two blocks per CU (partial tiles and a K tail in the last
+    case), through the public einsum against a float64 GPU reference."""
+    from pto_einsum import einsum
+
+    g = torch.Generator().manual_seed(M + K + N)
+    a = (torch.randn(M, K, generator=g) * 0.1).to(dtype).cuda()
+    b = (torch.randn(K, N, generator=g) * 0.1).to(dtype).cuda()
+    got = einsum("ij,jk->ik", a, b).double()
+    want = a.double() @ b.double()
+    rtol = 1e-4 if dtype == torch.float32 else 2e-3
+    assert float((got - want).abs().max()) <= rtol * float(want.abs().max())
+    assert torch.equal(einsum("ij,jk->ik", a, b), einsum("ij,jk->ik", a, b))  # deterministic split order
+
+
 def test_gemm_rejects_bad_tile():
     lib = abi.bind()
     d = launch.GemmDesc(dtype=launch.DT_F16, batch_shape=[1], a_bstride=[0], b_bstride=[0], c_bstride=[0],
