@@ -181,7 +181,9 @@ GemmChoice choose(const pe_gemm_desc& d, bool dl = false, int al = L_MN, int bl 
         // MI355X for batched 128^3 blocks and 2048^2 outputs at K = 128..512).
         c.bm = (d.M > 64 && d.N > 64) ? 128 : 64;
         const int64_t tiles128 = c.nbatch_total * ceil_div(d.M, 128) * ceil_div(d.N, 128);
-        if (c.bm == 128 && tiles128 <= PE_GEMM_SMALL_TILE_CUS * cus) c.bm = 64;
+        // (float32 only: the float16 64x64 tiles measured 1.1-3x slower than
+        // 128x128 on such grids, e.g. 1024^2 at K = 128: 17.2 against 5.5 us.)
+        if (c.bm == 128 && d.dtype == PE_F32 && tiles128 <= PE_GEMM_SMALL_TILE_CUS * cus) c.bm = 64;
         // Long-K grids that need a K split with either tile: 128x128 tiles
         // split to about two blocks per CU, each split at least 16 slabs
         // deep, beat 64x64 tiles (config 5.3, ts,sp->tp float32 with K = 4096:
@@ -267,8 +269,13 @@ GemmChoice choose(const pe_gemm_desc& d, bool dl = false, int al = L_MN, int bl 
     } else if (long_k_split > 0) {
         split = long_k_split;
     } else if (tiles < cus && c.nbatch_total * d.M * d.N < (int64_t(1) << 32)) {
-        // Fill about four blocks per CU, keeping at least four K slabs per split.
+        // At most about four blocks per CU and at least four K slabs per
+        // split; beyond one block per CU, split further only while each split
+        // keeps 16 slabs (the reduction reads every split's partial output
+        // back: 512^2 at K = 1024, 16 splits of 4 slabs 19.3 us, 4 of 16
+        // slabs 15.3 us; 256^3, 4 splits of 4 slabs, 7.4 us either way).
         split = std::min<int64_t>(ceil_div(4 * cus, tiles), std::max<int64_t>(1, d.K / (4 * bk)));
+        split = std::min<int64_t>(split, std::max<int64_t>(ceil_div(cus, tiles), d.K / (16 * bk)));
         split = std::max<int64_t>(1, std::min<int64_t>(split, 32));
     }
     int64_t kps = ceil_div(ceil_div(d.K, split), bk) * bk;
