@@ -183,7 +183,11 @@ GemmChoice choose(const pe_gemm_desc& d, bool dl = false, int al = L_MN, int bl 
         const int64_t tiles128 = c.nbatch_total * ceil_div(d.M, 128) * ceil_div(d.N, 128);
         // (float32 only: the float16 64x64 tiles measured 1.1-3x slower than
         // 128x128 on such grids, e.g. 1024^2 at K = 128: 17.2 against 5.5 us.)
-        if (c.bm == 128 && d.dtype == PE_F32 && tiles128 <= PE_GEMM_SMALL_TILE_CUS * cus) c.bm = 64;
+        // Nor where 128x128 tiles already give every CU one and K > 512
+        // (2048^2 float32 at K = 4096: 372 -> 344 us; at K = 1024: 95.5 -> 91.8).
+        if (c.bm == 128 && d.dtype == PE_F32 && tiles128 <= PE_GEMM_SMALL_TILE_CUS * cus &&
+            !(tiles128 >= cus && d.K > 512))
+            c.bm = 64;
         // Long-K grids that need a K split with either tile: 128x128 tiles
         // split to about two blocks per CU, each split at least 16 slabs
         // deep, beat 64x64 tiles (config 5.3, ts,sp->tp float32 with K = 4096:
