@@ -520,7 +520,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              "(the contraction would shard on its batch axes with no exchange; see DESIGN.md).",
+              "(the contraction would shard on its batch axes with no exchange between GPUs).",
               file=sys.stderr)
         sys.exit(2)
     import torch

@@ -15,9 +15,9 @@ For every case this writes, into ``oracle/_ref/`` only:
   (builder.py:705-709).
 
 No reference file is copied; the header is included from where it lies.
-``/root/reference`` is absent on the GPU box, so the built ``.so`` files
-travel there with the tree (``oracle/_ref/`` is git-ignored, not
-gpurun-ignored).  Run: ``python oracle/ref_build.py [-j N]``.
+``/root/reference`` is absent on the GPU machine, so the built ``.so`` files
+travel there with the working tree (``oracle/_ref/`` is kept out of version
+control only).  Run: ``python oracle/ref_build.py [-j N]``.
 """
 from __future__ import annotations
 
