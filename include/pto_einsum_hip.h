@@ -154,8 +154,12 @@ int pe_linear_attention(const pe_linattn_desc* d, const void* q, const void* k, 
  * "Option A"), reached from Python through einsum(..., reduce_solo_axes=True).
  *   dst[k] = sum over r of (float)src[sum_d k_d keep_stride[d] + sum_e r_e red_stride[e]]
  * with k the row-major index over keep_shape (dst contiguous float32) and r
- * over red_shape.  Each output sums its terms in row-major order of r from +0,
- * as a sequential loop (deterministic).  nred = 0 is a conversion to float32. */
+ * over red_shape.  Order (a function of the shapes only, so deterministic): the
+ * nterm terms of an output, row-major in r, are cut into C contiguous chunks (the
+ * first nterm % C one term longer); each chunk is summed from +0 and the partial
+ * sums are added in chunk order from +0; C = 1 (the sequential loop) when
+ * nterm <= 256 or nout >= 32768, else min(256, ceil(nterm / 256)).
+ * nred = 0 is a conversion to float32. */
 typedef struct pe_reduce_desc {
     int32_t dtype;                      /* PE_F32 or PE_F16 */
     int32_t nkeep;                      /* 0..PE_MAX_DIMS */

@@ -1,8 +1,11 @@
 """Opt-in single-operand reduction axes on the GPU.
 
-The reduction stage (pe_reduce_axes) is checked bit for bit against a
-sequential float32 loop on the CPU (its documented order: row-major over the
-reduced index, from +0); whole einsums are checked against float64
+The reduction stage (pe_reduce_axes) is checked bit for bit against float32
+loops on the CPU in its documented order: the terms of an output, row-major
+over the reduced index, cut into C contiguous chunks (the first nterm % C one
+term longer), each chunk summed from +0 and the partial sums added in chunk
+order from +0; C = 1 when nterm <= 256 or there are at least 32768 outputs,
+else min(256, ceil(nterm / 256)).  Whole einsums are checked against float64
 torch.einsum with the contraction tolerance (the reference has no result to
 compare with: it rejects these equations)."""
 import ctypes
@@ -15,26 +18,53 @@ from pto_einsum import abi, einsum, runtime
 
 pytestmark = pytest.mark.gpu
 
+CHUNK_TERMS, WIDE_OUTPUTS, CHUNK_THREADS = 256, 32768, 256
 
-def _seq_sum(x: np.ndarray, axes):
-    """Sequential float32 sum over `axes` (row-major order of the reduced
-    index, from +0), the other axes kept in order."""
+
+def _ordered_sum(x: np.ndarray, axes):
+    """float32 sum over `axes` in the chunked order above, the other axes
+    kept in order.  Each loop step adds one term to every output at once, so
+    the per-output order is sequential."""
     keep = [i for i in range(x.ndim) if i not in axes]
     xt = np.transpose(x, keep + list(axes)).astype(np.float32)
-    flat = xt.reshape(int(np.prod([x.shape[i] for i in keep], dtype=np.int64)), -1)
-    out = np.zeros(flat.shape[0], dtype=np.float32)
-    for r in range(flat.shape[0]):
+    nout = int(np.prod([x.shape[i] for i in keep], dtype=np.int64))
+    flat = xt.reshape(nout, -1)
+    nterm = flat.shape[1]
+    nchunk = 1 if nterm <= CHUNK_TERMS or nout >= WIDE_OUTPUTS else min(CHUNK_THREADS, -(-nterm // CHUNK_TERMS))
+    q, r = divmod(nterm, nchunk)
+    total = np.zeros(nout, dtype=np.float32)
+    t = 0
+    for c in range(nchunk):
+        acc = np.zeros(nout, dtype=np.float32)
+        for _ in range(q + (1 if c < r else 0)):
+            acc = acc + flat[:, t]
+            t += 1
+        total = total + acc
+    assert t == nterm
+    return total.reshape([x.shape[i] for i in keep])
+
+
+def test_ordered_sum_restates_the_plain_loop_for_one_chunk():
+    """The checker itself: with one chunk it is the scalar sequential loop."""
+    x = np.random.default_rng(1).standard_normal((3, 200)).astype(np.float32)
+    want = np.zeros(3, dtype=np.float32)
+    for i in range(3):
         acc = np.float32(0.0)
-        for v in flat[r]:
+        for v in x[i]:
             acc = np.float32(acc + v)
-        out[r] = acc
-    return out.reshape([x.shape[i] for i in keep])
+        want[i] = acc
+    assert np.array_equal(_ordered_sum(x, (1,)).view(np.uint32), want.view(np.uint32))
+    # more chunks: the same total to rounding, a different (chunked) order
+    y = np.random.default_rng(2).standard_normal((2, 5000)).astype(np.float32)
+    assert np.allclose(_ordered_sum(y, (1,)), y.astype(np.float64).sum(1), rtol=0, atol=1e-3)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16], ids=["f32", "f16"])
 @pytest.mark.parametrize("shape,axes,transpose", [((5, 7, 9), (1,), False), ((5, 7, 9), (0, 2), False),
                                                   ((6, 33), (1,), True), ((4, 3), (), False),
-                                                  ((3, 0, 2), (1,), False)])
+                                                  ((3, 0, 2), (1,), False),
+                                                  ((3, 70001), (1,), False), ((2, 37, 300), (1, 2), False),
+                                                  ((300, 5), (0,), True), ((40000, 300), (1,), False)])
 def test_reduce_axes_is_the_sequential_sum(dtype, shape, axes, transpose):
     from pto_einsum.builder import _reduce_operand
 
@@ -45,7 +75,7 @@ def test_reduce_axes_is_the_sequential_sum(dtype, shape, axes, transpose):
     if transpose:  # a non-contiguous view
         xd = x.t().contiguous().cuda().t()
     got = _reduce_operand(xd, subs, "".join(subs[i] for i in axes)).cpu().numpy()
-    want = _seq_sum(x.float().numpy(), axes)
+    want = _ordered_sum(x.float().numpy(), axes)
     assert got.dtype == np.float32 and got.shape == want.shape
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
@@ -58,6 +88,7 @@ EQS = [
     ("bij,bjk->bk", (4, 60, 70), (4, 70, 80)),
     ("abc,cd->ad", (20, 30, 40), (40, 50)),
     ("i,j->", (300,), (400,)),
+    ("ij,jk->k", (70000, 8), (8, 40)),
 ]
 
 
