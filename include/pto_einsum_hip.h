@@ -183,6 +183,20 @@ int pe_einsum_teardown(void* ws);
 int pe_einsum_run(const pe_einsum_plan* p, const void* in0, const void* in1, float* out,
                   void* stream);
 
+/* Allocation-free plan executor.  No counterpart in the reference: it is for
+ * callers that cannot allocate (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  Same kernels and results as
+ * pe_einsum_exec, but the workspace is a static device array of
+ * PE_NOALLOC_SCRATCH_BYTES that each GPU the library runs on holds until the
+ * process ends; no hipMalloc, hipFree or allocating library call is made.
+ * A plan whose workspace exceeds the limit returns PE_ERR_WORKSPACE (message
+ * in pe_last_error) without launching.  Every call on one GPU shares that
+ * GPU's array: calls that overlap on one GPU (different streams, or
+ * different host threads without ordering) race. */
+#define PE_NOALLOC_SCRATCH_BYTES (64ll << 20)
+int pe_einsum_exec_noalloc(const pe_einsum_plan* p, const void* in0, const void* in1, float* out,
+                           void* stream);
+
 const char* pe_last_error(void);        /* message for the calling thread's last failure */
 int pe_device_cu_count(void);           /* compute units of the current device */
 const char* pe_version(void);

@@ -126,6 +126,61 @@ extern "C" int pe_einsum_exec(const pe_einsum_plan* p, const void* in0, const vo
     return PE_OK;
 }
 
+// ------------------------------------------------ allocation-free executor --
+//
+// Device scratch of pe_einsum_exec_noalloc: a file-scope device array that
+// every GPU this library runs on holds (PE_NOALLOC_SCRATCH_BYTES of it) until
+// the process ends.  In host code `scratch` names a host-side stand-in, not a
+// device address: the device address is looked up once per device with
+// hipGetSymbolAddress (with that device current) and only that pointer is
+// ever handed to a launch.
+static __device__ __align__(256) char scratch[PE_NOALLOC_SCRATCH_BYTES];
+
+namespace pe {
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {nullptr};
+
+// Device address of the current device's copy of `scratch`.
+int device_scratch(void** out) {
+    int dev = 0;
+    PE_CHECK_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices) return fail(PE_ERR_UNSUPPORTED, "exec_noalloc: device ordinal above 63");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* ptr = nullptr;
+        PE_CHECK_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+        if (!ptr) return fail(PE_ERR_WORKSPACE, "exec_noalloc: no device address for the scratch array");
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return PE_OK;
+}
+
+}  // namespace
+}  // namespace pe
+
+extern "C" int pe_einsum_exec_noalloc(const pe_einsum_plan* p, const void* in0, const void* in1, float* out,
+                                      void* stream) {
+    using namespace pe;
+    if (!p) return fail(PE_ERR_INVALID, "exec_noalloc: null plan");
+    const int64_t need = plan_workspace_bytes(*p);
+    if (need > int64_t(PE_NOALLOC_SCRATCH_BYTES))
+        return fail(PE_ERR_WORKSPACE, "exec_noalloc: the plan needs " + std::to_string(need) +
+                                          " bytes of workspace, above the " +
+                                          std::to_string(int64_t(PE_NOALLOC_SCRATCH_BYTES)) +
+                                          "-byte scratch limit; use run_einsum_setup / pe_einsum_exec");
+    void* ws = nullptr;
+    const int st = device_scratch(&ws);
+    if (st != PE_OK) return st;
+    // Every workspace region the plan uses (operand gathers, the staged
+    // result, split-K partials) is written in full before it is read, so no
+    // clearing is needed and the previous call's contents are harmless.
+    return pe_einsum_exec(p, in0, in1, out, ws, stream);
+}
+
 extern "C" int pe_einsum_run(const pe_einsum_plan* p, const void* in0, const void* in1, float* out,
                              void* stream) {
     void* ws = pe_einsum_setup(p, stream);

@@ -100,6 +100,26 @@ def product_desc(d: launch.ProductDesc) -> ProductDesc:
     return c
 
 
+def einsum_plan(p: launch.LaunchPlan) -> EinsumPlan:
+    """The ``pe_einsum_plan`` of a launch plan (the struct the generated
+    per-shape sources fill in, built here for direct calls)."""
+    c = EinsumPlan()
+    c.route = p.route
+    if p.route == launch.ROUTE_PRODUCT:
+        c.product = product_desc(p.product)
+        return c
+    c.gather0, c.gather1, c.scatter_out = int(p.gather0), int(p.gather1), int(p.scatter_out)
+    c.gemm = gemm_desc(p.gemm)
+    if p.gather0:
+        c.perm0 = permute_desc(p.perm0)
+    if p.gather1:
+        c.perm1 = permute_desc(p.perm1)
+    if p.scatter_out:
+        c.perm_out = permute_desc(p.perm_out)
+    c.ws0_off, c.ws1_off, c.wsout_off, c.ws_bytes = p.ws0_off, p.ws1_off, p.wsout_off, p.ws_bytes
+    return c
+
+
 def bind(lib=None):
     """Set argtypes/restypes of the core launchers on the loaded core library."""
     lib = lib or runtime.core()
@@ -114,11 +134,12 @@ def bind(lib=None):
     lib.pe_einsum_setup.restype = vp
     lib.pe_einsum_teardown.argtypes = [vp]
     lib.pe_einsum_run.argtypes = [ctypes.POINTER(EinsumPlan), vp, vp, vp, vp]
+    lib.pe_einsum_exec_noalloc.argtypes = [ctypes.POINTER(EinsumPlan), vp, vp, vp, vp]
     lib.pe_linear_attention.argtypes = [ctypes.POINTER(LinAttnDesc), vp, vp, vp, vp, vp, vp, ctypes.c_int64, vp]
     lib.pe_linear_attention_workspace_bytes.argtypes = [ctypes.POINTER(LinAttnDesc)]
     lib.pe_linear_attention_workspace_bytes.restype = ctypes.c_int64
     lib.pe_reduce_axes.argtypes = [ctypes.POINTER(ReduceDesc), vp, vp, vp]
     for f in ("pe_product", "pe_permute", "pe_gemm", "pe_einsum_exec", "pe_einsum_teardown", "pe_einsum_run",
-              "pe_linear_attention", "pe_reduce_axes"):
+              "pe_einsum_exec_noalloc", "pe_linear_attention", "pe_reduce_axes"):
         getattr(lib, f).restype = ctypes.c_int
     return lib

@@ -141,3 +141,16 @@ def test_descriptor_validation_rejects_out_of_bounds():
     q = abi.ProductDesc()
     q.dtype, q.ndims, q.a_numel, q.b_numel = 3, 0, 1, 1
     assert lib.pe_product(ctypes.byref(q), None, None, None, None) == -3
+
+
+def test_noalloc_rejects_oversized_plan_without_launch():
+    """The allocation-free executor refuses a plan whose workspace exceeds its
+    static scratch, before any device call (so this runs without a GPU)."""
+    lib = abi.bind()
+    b = EinsumBuilder("abc,cd->adb", [(512, 512, 64), (64, 512)], torch.float32)
+    b.parse_equation()
+    b.generate_code()
+    assert b.launch_plan.scatter_out and b.launch_plan.ws_bytes > (64 << 20)
+    plan = abi.einsum_plan(b.launch_plan)
+    assert lib.pe_einsum_exec_noalloc(ctypes.byref(plan), None, None, None, None) == -4
+    assert b"scratch limit" in lib.pe_last_error()
