@@ -8,13 +8,19 @@ steps (2*b*i*j*k flops per step).  ``roofline`` relates the GEMM kernel's
 average launch time (HIP events recorded around each launch on the launch
 stream) to the float32 MFMA peak.  ``cpu_baseline`` times the reference CPU
 route (cpu_einsum.h compiled by oracle/ref_build.py; the C restatement in
-oracle/ when that build is absent) on one of the 16 batches.
+oracle/ when that build is absent) on the whole of config 2, one thread.
+
+Cache: MI355X has a 256 MB Infinity Cache in front of HBM.  Every timed case
+therefore rotates through enough copies of its operands and output (at least
+1 GiB in total, four times the cache) that each call reads operands no call
+has touched for over 768 MB of traffic: the figures are HBM figures, not
+cache figures.  The headline steps rotate the same way.
 
 ``per_config`` adds every other BASELINE equation at full size with its own
 binding roof (HBM bytes or MFMA flops).  Those kernels run for tens of
-microseconds, less than one Python-level call costs, so each is captured once
-in a HIP graph and the graph is replayed between two events: the figure is the
-GPU time of the einsum's launches.
+microseconds, less than one Python-level call costs, so the rotation's calls
+are captured once in a HIP graph and the graph is replayed between two
+events: the figure is the GPU time per einsum.
 
 ``large_f16`` times 8192^3 float16 contractions (float32 output) in the
 NN and NT layouts on the dense float16 MFMA roof, with torch.matmul (the
@@ -26,15 +32,19 @@ per launch) and replayed as one HIP graph (``pto_einsum.StageGraph``).
 
 ``roofline.traffic`` (HBM bytes per launch of the headline GEMM) is read from
 profiles/gemm_f32_config2_traffic.json, written from two rocprofv3 --pmc runs
-(FETCH_SIZE, WRITE_SIZE) of this script, scaled by the same counters on
-``--copy-probe`` (a plain copy of known size).
+(FETCH_SIZE, WRITE_SIZE) of ``bench.py --profile 2``, scaled by the same
+counters on ``--copy-probe`` (a plain copy of known size); the file names
+the kernel it was measured on, and the line carries that name beside it.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-configs]
+       python bench.py --profile CASE   # one case, eager calls, for rocprofv3
+       python bench.py --list-cases
        python bench.py --copy-probe     # counter calibration: one 1 GiB copy
 """
 import argparse
 import ctypes
 import json
+import math
 import os
 import statistics
 import sys
@@ -45,6 +55,8 @@ sys.path.insert(0, os.path.join(ROOT, "pto-einsum_amd"))
 
 PEAK_HBM_GBS = 8000.0
 PEAK_TFLOPS = {"f32": 157.3, "f16": 2516.6}
+ROTATE_BYTES = 1 << 30          # rotated working set per timed case (4x the Infinity Cache)
+MAX_SETS = 2048
 
 
 def log(msg):
@@ -57,20 +69,41 @@ def parse():
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-configs", action="store_true", help="headline workload only")
-    ap.add_argument("--cpu-sample-batches", type=int, default=1)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
-                    help="wall-time budget of the CPU-baseline sample")
+                    help="wall-time budget of the CPU baseline (at least one whole call)")
+    ap.add_argument("--profile", metavar="CASE",
+                    help="run one case (see --list-cases) as eager rotated calls and exit")
+    ap.add_argument("--list-cases", action="store_true")
     ap.add_argument("--copy-probe", action="store_true",
                     help="run a plain 1 GiB device copy (counter calibration) and exit")
     return ap.parse_args()
 
 
-def time_runner(run, a, b, steps, warmup):
-    """Per-launch HIP-event times (ms) and wall time of the timed region."""
+# ------------------------------------------------------------------ timing --
+
+def n_sets(set_bytes):
+    """Copies of a case's operands + output that make a >= 1 GiB rotation."""
+    if set_bytes >= ROTATE_BYTES:
+        return 1
+    return int(min(MAX_SETS, max(2, math.ceil(ROTATE_BYTES / max(1, set_bytes)))))
+
+
+def replicate(tensors, n):
+    """n copies (the first the originals) of every tensor, on the GPU."""
+    sets = [tuple(tensors)]
+    for _ in range(n - 1):
+        sets.append(tuple(t.clone() for t in tensors))
+    return sets
+
+
+def time_runner(run, sets, steps, warmup):
+    """Headline timing: per-launch HIP-event times (ms) and the wall time of
+    the timed region; step i runs on operand set i % len(sets)."""
     import torch
 
-    for _ in range(warmup):
-        run(a, b)
+    for i in range(warmup):
+        run(*sets[i % len(sets)])
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
@@ -78,9 +111,9 @@ def time_runner(run, a, b, steps, warmup):
     t1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0.record(stream)
-    for s, e in ev:
+    for i, (s, e) in enumerate(ev):
         s.record(stream)
-        run(a, b)
+        run(*sets[(warmup + i) % len(sets)])
         e.record(stream)
     t1.record(stream)
     torch.cuda.synchronize()
@@ -88,42 +121,46 @@ def time_runner(run, a, b, steps, warmup):
     return per, t0.elapsed_time(t1)
 
 
-def time_graph(run, a, b, steps, warmup, out_bytes):
-    """GPU time (ms) of one einsum: `reps` calls are captured in one HIP graph
-    (graph launch overhead paid once per replay), the graph is replayed
-    `steps` times between events, and the median per-call time is returned."""
+def time_graph(call, sets, reps=5):
+    """GPU time (ms) per call: one call per operand set captured in one HIP
+    graph, the graph replayed between two events `reps` times; the median
+    replay time divided by the number of calls."""
     import torch
 
-    reps = int(max(1, min(20, (8 << 30) // max(1, out_bytes))))
-    for _ in range(max(2, warmup)):
-        run(a, b)
+    for s in sets[:2]:
+        call(*s)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
-        for _ in range(reps):
-            run(a, b)
-    for _ in range(2):
-        g.replay()
+        for s in sets:
+            call(*s)
+    g.replay()
     torch.cuda.synchronize()
     per = []
-    for _ in range(max(3, steps // 4)):
+    for _ in range(reps):
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
         e0.record()
         g.replay()
         e1.record()
         torch.cuda.synchronize()
-        per.append(e0.elapsed_time(e1) / reps)
+        per.append(e0.elapsed_time(e1) / len(sets))
     del g
-    torch.cuda.empty_cache()
     return statistics.median(per)
+
+
+def run_eager(call, sets, calls):
+    """Profiling mode: `calls` eager calls rotating over the sets."""
+    import torch
+
+    for i in range(calls):
+        call(*sets[i % len(sets)])
+    torch.cuda.synchronize()
 
 
 def copy_probe():
     """A 1 GiB float32 copy through the core library's permutation launcher
     (identity permutation = plain copy): reads and writes exactly 1 GiB."""
-    import ctypes
-
     import torch
 
     from pto_einsum import abi, launch
@@ -145,21 +182,39 @@ def traffic_from_profile():
     path = os.path.join(ROOT, "profiles", "gemm_f32_config2_traffic.json")
     try:
         with open(path) as f:
-            return json.load(f).get("hbm_bytes_per_launch")
+            d = json.load(f)
     except (OSError, ValueError):
-        return None
+        return None, None
+    src = f"profiles/gemm_f32_config2_traffic.json ({d.get('kernel', '?')}, commit {d.get('commit', '?')})"
+    return d.get("hbm_bytes_per_launch"), src
+
+
+# ------------------------------------------------------------------- cases --
+
+def rope_table(s, d):
+    import torch
+
+    pos = torch.arange(s, dtype=torch.float64)[:, None]
+    i = torch.arange(d, dtype=torch.float64)[None, :] % (d // 2)
+    theta = 10000.0 ** (-2.0 * i / d)
+    return torch.cos(pos * theta).to(torch.float16)
+
+
+def decay(t, gamma):
+    import torch
+
+    i = torch.arange(t, dtype=torch.float64)
+    d = (i[:, None] - i[None, :])
+    return torch.where(d >= 0, gamma ** d.clamp(min=0), torch.zeros(())).float()
 
 
 def config_list():
+    """BASELINE configs other than the headline: (name, equation, operand
+    generator, roof dtype)."""
     import torch
 
     def randn(shape, g, scale=1.0, dtype=torch.float32):
         return (torch.randn(shape, generator=g) * scale).to(dtype)
-
-    def decay(t, gamma):
-        i = torch.arange(t, dtype=torch.float64)
-        d = (i[:, None] - i[None, :])
-        return torch.where(d >= 0, gamma ** d.clamp(min=0), torch.zeros(())).float()
 
     f16 = torch.float16
     return [
@@ -195,16 +250,94 @@ def transpose_list():
     ]
 
 
-def time_transposes(dev, steps, warmup):
-    """GPU time of each standalone transpose (HIP graph replay, as for the
-    per-config figures) with its HBM roof: one read and one write of every
-    element."""
+GDN_EQS = (("kkt", "bihd,bjhd->bihj"), ("wy_fast", "bihj,bjhd->bihd"),
+           ("chunk_h kv", "bvhd,bvhe->bhde"), ("chunk_o inter", "bvhd,bhde->bvhe"))
+
+
+def gdn_list():
+    """The GDN contraction set (float32, chunk = d = 128) at the sizes the
+    reference measures it on (IMPLEMENTATION.md:700-782: b x H = 16x16, 64x16,
+    16x48; b = folded chunks): (label, equation, shape0, shape1)."""
+    rows = []
+    for b, H in ((16, 16), (64, 16), (16, 48)):
+        for name, eq in GDN_EQS:
+            s1 = (b, H, 128, 128) if eq == "bvhd,bhde->bvhe" else (b, 128, H, 128)
+            rows.append((f"{name} {b}x{H}", eq, (b, 128, H, 128), s1))
+    return rows
+
+
+def work(eq, a, b):
+    """(flops, compulsory bytes) of one einsum: 2*I*L0*L1*C (or N for a
+    product) and inputs read once plus the float32 output written once."""
+    from math import prod
+
+    t0, rest = eq.split(",")
+    t1, to = rest.split("->")
+    size = dict(zip(t0, a.shape))
+    size.update(zip(t1, b.shape))
+    out = prod(size[x] for x in to)
+    C = prod(size[x] for x in (set(t0) & set(t1)) - set(to))
+    flops = 2 * out * C if C > 1 else out
+    nbytes = a.numel() * a.element_size() + b.numel() * b.element_size() + out * 4
+    return flops, nbytes
+
+
+def roofline(flops, nbytes, t_ms, dtype):
+    tflops = flops / (t_ms * 1e-3) / 1e12
+    gbs = nbytes / (t_ms * 1e-3) / 1e9
+    t_mfma = flops / (PEAK_TFLOPS[dtype] * 1e12)
+    t_hbm = nbytes / (PEAK_HBM_GBS * 1e9)
+    if t_mfma >= t_hbm:
+        return dict(bound="mfma", achieved=round(tflops, 3), peak=PEAK_TFLOPS[dtype], unit="TFLOP/s",
+                    frac=round(tflops / PEAK_TFLOPS[dtype], 4)), tflops, gbs
+    return dict(bound="hbm", achieved=round(gbs, 1), peak=PEAK_HBM_GBS, unit="GB/s",
+                frac=round(gbs / PEAK_HBM_GBS, 4)), tflops, gbs
+
+
+class Case:
+    """One timed workload: `prepare(dev)` returns (call, operand tuple,
+    set bytes); `call(*operands)` enqueues it once."""
+
+    def __init__(self, name, prepare, finish):
+        self.name, self.prepare, self.finish = name, prepare, finish
+
+
+def einsum_case(name, eq, gen, dt, seed, label=None):
     import torch
 
     from pto_einsum import EinsumBuilder
 
-    rows = []
-    for label, eq, shapes, dtype, entry in transpose_list():
+    def prepare(dev):
+        g = torch.Generator().manual_seed(seed)
+        x, y = gen(g)
+        x, y = x.to(dev), y.to(dev)
+        r = EinsumBuilder(eq, [tuple(x.shape), tuple(y.shape)], x.dtype).build()
+        out_bytes = r(x, y).numel() * 4
+        return r, (x, y), x.numel() * x.element_size() + y.numel() * y.element_size() + out_bytes
+
+    def finish(ms, operands, nsets):
+        x, y = operands
+        f, nb = work(eq, x, y)
+        rf, tf, gb = roofline(f, nb, ms, dt)
+        row = dict(config=name, equation=eq, dtype=dt, us=round(ms * 1e3, 2), tflops=round(tf, 3),
+                   gbs=round(gb, 1), roof=rf["bound"], frac=rf["frac"], sets=nsets)
+        if label:
+            row = dict(label, **row)
+        log(f"bench: {name} {eq} {ms * 1e3:.1f} us  {tf:.2f} TFLOP/s  {gb:.0f} GB/s  "
+            f"{rf['bound']} {rf['frac'] * 100:.1f}%  ({nsets} rotated sets)")
+        return row
+
+    return Case(name, prepare, finish)
+
+
+def transpose_case(label, eq, shapes, dtype, entry):
+    import torch
+
+    from pto_einsum import EinsumBuilder
+
+    info = {}
+
+    def prepare(dev):
         builder = EinsumBuilder(eq, [tuple(x) for x in shapes], dtype)
         builder.build()
         rec = builder.recipe
@@ -221,80 +354,145 @@ def time_transposes(dev, steps, warmup):
         x = torch.randn(src_shape, generator=g).to(src_dtype).to(dev)
         y = torch.empty([src_shape[p] for p in perm], dtype=src_dtype, device=dev)
         fn = getattr(builder.lib, entry)
+        info.update(builder=builder, src_shape=src_shape, perm=perm, src_dtype=src_dtype)
 
-        def run(a, b, fn=fn, x=x, y=y):
+        def call(x, y):
             rc = fn(ctypes.cast(x.data_ptr(), fn.argtypes[0]), ctypes.cast(y.data_ptr(), fn.argtypes[1]),
                     ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
             if rc != 0:
                 raise RuntimeError(f"{entry} failed ({rc})")
 
-        km = time_graph(run, None, None, max(10, steps), max(3, warmup // 2), y.numel() * y.element_size())
+        return call, (x, y), 2 * x.numel() * x.element_size()
+
+    def finish(ms, operands, nsets):
+        x, _ = operands
         nbytes = 2 * x.numel() * x.element_size()
-        gbs = nbytes / (km * 1e-3) / 1e9
-        rows.append(dict(transpose=label, equation=eq, dtype=str(src_dtype).replace("torch.", ""),
-                         shape=list(src_shape), perm=list(perm), us=round(km * 1e3, 2), gbs=round(gbs, 1),
-                         roof="hbm", frac=round(gbs / PEAK_HBM_GBS, 4)))
-        log(f"bench: transpose {label} of {eq} {src_shape} {km * 1e3:.1f} us  {gbs:.0f} GB/s  "
-            f"hbm {gbs / PEAK_HBM_GBS * 100:.1f}%")
-        del x, y, builder
-        torch.cuda.empty_cache()
-    return rows
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        log(f"bench: transpose {label} of {eq} {info['src_shape']} {ms * 1e3:.1f} us  {gbs:.0f} GB/s  "
+            f"hbm {gbs / PEAK_HBM_GBS * 100:.1f}%  ({nsets} rotated sets)")
+        return dict(transpose=label, equation=eq, dtype=str(info["src_dtype"]).replace("torch.", ""),
+                    shape=list(info["src_shape"]), perm=list(info["perm"]), us=round(ms * 1e3, 2),
+                    gbs=round(gbs, 1), roof="hbm", frac=round(gbs / PEAK_HBM_GBS, 4), sets=nsets)
+
+    return Case("T" + ".".join(label.split()[:2]), prepare, finish)
 
 
-def time_fused_chain(dev, steps, warmup):
+T5, N5 = 4096, 128
+
+
+def chain_case(precise):
     """BASELINE config 5's linear-attention chain in one fused launch
     (pto_einsum.linear_attention): q, k float16 normal(0, 1/sqrt(128)), v
     float16 normal(0, 1), the causal decay mask gamma^(t-s), gamma = 0.995,
     in float32; t = s = 4096, n = p = 128.  The default launch computes P.V
-    as three bfloat16 MFMA terms of the split P and V; ``precise_us`` is the
-    same chain with P.V on float32 MFMAs.  The roof is the larger of the
-    compulsory HBM bytes (q, k, v, m read once, out written once) at 8 TB/s
-    and the MFMAs the default launch issues for the dense chain (2*T*S*N
-    float16 flops plus 3 * 2*T*S*P bfloat16 flops at the 16-bit peak); masked
-    blocks that are zero are skipped, so the causal case does less."""
+    as three bfloat16 MFMA terms of the split P and V; ``precise`` puts P.V on
+    float32 MFMAs.  The roof is the larger of the compulsory HBM bytes (q, k,
+    v, m read once, out written once) at 8 TB/s and the MFMAs the launch
+    issues for the dense chain (2*T*S*N float16 flops plus, for the default,
+    3 * 2*T*S*P bfloat16 flops at the 16-bit peak, for precise 2*T*S*P at
+    the float32 peak); zero mask blocks are skipped, so the causal case does
+    less."""
     import torch
 
     from pto_einsum import linear_attention
 
-    T = S = 4096
-    N = P = 128
-    g = torch.Generator().manual_seed(105)
-    q = (torch.randn(T, N, generator=g) * N ** -0.5).half().to(dev)
-    k = (torch.randn(S, N, generator=g) * N ** -0.5).half().to(dev)
-    v = torch.randn(S, P, generator=g).half().to(dev)
-    i = torch.arange(T, dtype=torch.float64)
-    d = i[:, None] - i[None, :]
-    m = torch.where(d >= 0, 0.995 ** d.clamp(min=0), torch.zeros(())).float().to(dev)
-    km = time_graph(lambda a, b: linear_attention(q, k, v, m), None, None, max(10, steps), max(3, warmup // 2),
-                    T * P * 4)
-    kp = time_graph(lambda a, b: linear_attention(q, k, v, m, precise=True), None, None, max(10, steps),
-                    max(3, warmup // 2), T * P * 4)
-    flops = 2 * T * S * N + T * S + 2 * T * S * P
-    nbytes = (q.numel() + k.numel() + v.numel()) * 2 + m.numel() * 4 + T * P * 4
-    hbm_ms = nbytes / (PEAK_HBM_GBS * 1e9) * 1e3
-    mfma_ms = (2 * T * S * N + 3 * 2 * T * S * P) / (PEAK_TFLOPS["f16"] * 1e12) * 1e3
-    floor_ms = max(hbm_ms, mfma_ms)
-    return dict(config="5.F", equation="tn,sn,sp,ts->tp (fused)", dtype="f16 q/k, f32 chain (P.V as 3 bf16 terms)",
-                us=round(km * 1e3, 2), tflops=round(flops / (km * 1e-3) / 1e12, 3),
-                gbs=round(nbytes / (km * 1e-3) / 1e9, 1), roof="hbm" if hbm_ms >= mfma_ms else "mfma",
-                frac=round(floor_ms / km, 4), precise_us=round(kp * 1e3, 2))
+    T = S = T5
+    N = P = N5
+
+    def prepare(dev):
+        g = torch.Generator().manual_seed(105)
+        q = (torch.randn(T, N, generator=g) * N ** -0.5).half().to(dev)
+        k = (torch.randn(S, N, generator=g) * N ** -0.5).half().to(dev)
+        v = torch.randn(S, P, generator=g).half().to(dev)
+        m = decay(T, 0.995).to(dev)
+        nbytes = (q.numel() + k.numel() + v.numel()) * 2 + m.numel() * 4 + T * P * 4
+
+        def call(q, k, v, m):
+            linear_attention(q, k, v, m, precise=precise)
+
+        return call, (q, k, v, m), nbytes
+
+    def finish(ms, operands, nsets):
+        flops = 2 * T * S * N + T * S + 2 * T * S * P
+        nbytes = T * N * 2 * 2 + S * P * 2 + T * S * 4 + T * P * 4
+        hbm_ms = nbytes / (PEAK_HBM_GBS * 1e9) * 1e3
+        if precise:
+            mfma_ms = (2 * T * S * N / PEAK_TFLOPS["f16"] + 2 * T * S * P / PEAK_TFLOPS["f32"]) / 1e12 * 1e3
+        else:
+            mfma_ms = (2 * T * S * N + 3 * 2 * T * S * P) / (PEAK_TFLOPS["f16"] * 1e12) * 1e3
+        floor_ms = max(hbm_ms, mfma_ms)
+        row = dict(config="5.F" + (" precise" if precise else ""), equation="tn,sn,sp,ts->tp (fused)",
+                   dtype="f16 q/k, f32 chain, P.V " + ("f32 MFMA" if precise else "3 bf16 terms"),
+                   us=round(ms * 1e3, 2), tflops=round(flops / (ms * 1e-3) / 1e12, 3),
+                   gbs=round(nbytes / (ms * 1e-3) / 1e9, 1), roof="hbm" if hbm_ms >= mfma_ms else "mfma",
+                   frac=round(floor_ms / ms, 4), floor_us=round(floor_ms * 1e3, 2), sets=nsets)
+        log(f"bench: config {row['config']} tn,sn,sp,ts->tp {ms * 1e3:.1f} us (floor {floor_ms * 1e3:.1f} us, "
+            f"{row['roof']} {row['frac'] * 100:.1f}%)  ({nsets} rotated sets)")
+        return row
+
+    return Case("5.Fp" if precise else "5.F", prepare, finish)
 
 
-GDN_EQS = (("kkt", "bihd,bjhd->bihj"), ("wy_fast", "bihj,bjhd->bihd"),
-           ("chunk_h kv", "bvhd,bvhe->bhde"), ("chunk_o inter", "bvhd,bhde->bvhe"))
+def large_f16_cases():
+    import torch
+
+    n = 8192
+
+    def gen(g):
+        return ((torch.randn(n, n, generator=g) / 64).half(), (torch.randn(n, n, generator=g) / 64).half())
+
+    return [einsum_case(f"f16{lab}", eq, gen, "f16", 77, dict(shape=f"{n}^3 {lab}"))
+            for eq, lab in (("ij,jk->ik", "NN"), ("ik,jk->ij", "NT"))]
 
 
-def gdn_list():
-    """The GDN contraction set (float32, chunk = d = 128) at the sizes the
-    reference measures it on (IMPLEMENTATION.md:700-782: b x H = 16x16, 64x16,
-    16x48; b = folded chunks): (label, equation, shape0, shape1)."""
-    rows = []
-    for b, H in ((16, 16), (64, 16), (16, 48)):
-        for name, eq in GDN_EQS:
-            s1 = (b, H, 128, 128) if eq == "bvhd,bhde->bvhe" else (b, 128, H, 128)
-            rows.append((f"{name} {b}x{H}", eq, (b, 128, H, 128), s1))
-    return rows
+def gdn_cases():
+    import torch
 
+    out = []
+    for i, (label, eq, s0, s1) in enumerate(gdn_list()):
+        def gen(g, s0=s0, s1=s1):
+            return (torch.randn(s0, generator=g) * 128 ** -0.5, torch.randn(s1, generator=g) * 128 ** -0.5)
+
+        out.append(einsum_case("gdn." + label.replace(" ", "."), eq, gen, "f32", 200 + i,
+                               dict(gdn=label, shapes=[list(s0), list(s1)])))
+    return out
+
+
+def all_cases():
+    import torch
+
+    head = einsum_case("2", "bji,bjk->bik",
+                       lambda g: (torch.randn((16, 777, 1000), generator=g), torch.randn((16, 777, 1536), generator=g)),
+                       "f32", 2)
+    groups = {"headline": [head],
+              "per_config": [einsum_case(n, e, gen, d, 100 + i) for i, (n, e, gen, d) in enumerate(config_list())]
+              + [chain_case(False), chain_case(True)],
+              "transposes": [transpose_case(*t) for t in transpose_list()],
+              "large_f16": large_f16_cases(),
+              "gdn": gdn_cases()}
+    return groups
+
+
+def measure(case, dev, steps, warmup, profile_calls=0):
+    """Rotated timing of one case: returns its row (or runs it eagerly for a
+    profiler when profile_calls > 0)."""
+    import torch
+
+    call, operands, set_bytes = case.prepare(dev)
+    nsets = n_sets(set_bytes)
+    sets = replicate(operands, nsets)
+    if profile_calls:
+        log(f"bench: profiling {case.name}: {profile_calls} eager calls over {nsets} rotated sets")
+        run_eager(call, sets, profile_calls)
+        return None
+    ms = time_graph(call, sets, reps=max(3, steps // 6))
+    row = case.finish(ms, operands, nsets)
+    del sets, operands, call
+    torch.cuda.empty_cache()
+    return row
+
+
+# ------------------------------------------------------------ stage graphs --
 
 def time_eager(fn, iters):
     """GPU-side time (ms) per call of `fn` issued back to back from Python:
@@ -333,30 +531,16 @@ def time_stage_graph(fn, iters):
     return e0.elapsed_time(e1) / iters
 
 
-def time_gdn(dev, steps, warmup):
-    """Per-contraction GPU times of the GDN set, then two stage sequences
-    issued eagerly (one Python call per launch) and as one StageGraph replay:
-    the seven folded-batch contractions of one GDN forward (b = 16, H = 16)
-    and the chunk_h recurrence (B = 1, T = 1024, H = 32: per chunk two
-    contractions and four elementwise ops, eight chunks in sequence)."""
+def time_gdn_stages(dev, steps):
+    """Two GDN stage sequences issued eagerly (one Python call per launch)
+    and as one StageGraph replay: the seven folded-batch contractions of one
+    GDN forward (b = 16, H = 16) and the chunk_h recurrence (B = 1, T = 1024,
+    H = 32: per chunk two contractions and four elementwise ops, eight chunks
+    in sequence).  These measure launch overhead, so they run on one set of
+    operands (their working sets are cache-sized by construction)."""
     import torch
 
-    from pto_einsum import EinsumBuilder, einsum
-
-    rows = []
-    for label, eq, s0, s1 in gdn_list():
-        g = torch.Generator().manual_seed(200 + len(rows))
-        x = (torch.randn(s0, generator=g) * 128 ** -0.5).to(dev)
-        y = (torch.randn(s1, generator=g) * 128 ** -0.5).to(dev)
-        r = EinsumBuilder(eq, [s0, s1], torch.float32).build()
-        f, nb = work(eq, x, y)
-        km = time_graph(r, x, y, max(10, steps), max(3, warmup // 2), r(x, y).numel() * 4)
-        rf, tf, gb = roofline(f, nb, km, "f32")
-        rows.append(dict(gdn=label, equation=eq, dtype="f32", shapes=[list(s0), list(s1)], us=round(km * 1e3, 2),
-                         tflops=round(tf, 3), gbs=round(gb, 1), roof=rf["bound"], frac=rf["frac"]))
-        log(f"bench: gdn {label} {eq} {km * 1e3:.1f} us  {tf:.2f} TFLOP/s  {gb:.0f} GB/s  "
-            f"{rf['bound']} {rf['frac'] * 100:.1f}%")
-        del x, y, r
+    from pto_einsum import einsum
 
     g = torch.Generator().manual_seed(300)
     shape = (16, 128, 16, 128)
@@ -396,78 +580,30 @@ def time_gdn(dev, steps, warmup):
         log(f"bench: {label}: eager {eager * 1e3:.1f} us, graph replay {replay * 1e3:.1f} us "
             f"({eager / replay:.2f}x)")
     torch.cuda.empty_cache()
-    return rows, seqs
+    return seqs
 
 
-def rope_table(s, d):
+def time_torch_matmul(dev):
+    """torch.matmul (hipBLASLt, float16 output) at 8192^3 NN / NT beside the
+    large float16 contractions, rotating two operand sets."""
     import torch
 
-    pos = torch.arange(s, dtype=torch.float64)[:, None]
-    i = torch.arange(d, dtype=torch.float64)[None, :] % (d // 2)
-    theta = 10000.0 ** (-2.0 * i / d)
-    return torch.cos(pos * theta).to(torch.float16)
-
-
-def work(eq, a, b):
-    """(flops, compulsory bytes) of one einsum: 2*I*L0*L1*C (or N for a
-    product) and inputs read once plus the float32 output written once."""
-    from math import prod
-
-    t0, rest = eq.split(",")
-    t1, to = rest.split("->")
-    size = dict(zip(t0, a.shape))
-    size.update(zip(t1, b.shape))
-    out = prod(size[x] for x in to)
-    C = prod(size[x] for x in (set(t0) & set(t1)) - set(to))
-    flops = 2 * out * C if C > 1 else out
-    nbytes = a.numel() * a.element_size() + b.numel() * b.element_size() + out * 4
-    return flops, nbytes
-
-
-def roofline(flops, nbytes, t_ms, dtype):
-    tflops = flops / (t_ms * 1e-3) / 1e12
-    gbs = nbytes / (t_ms * 1e-3) / 1e9
-    t_mfma = flops / (PEAK_TFLOPS[dtype] * 1e12)
-    t_hbm = nbytes / (PEAK_HBM_GBS * 1e9)
-    if t_mfma >= t_hbm:
-        return dict(bound="mfma", achieved=round(tflops, 3), peak=PEAK_TFLOPS[dtype], unit="TFLOP/s",
-                    frac=round(tflops / PEAK_TFLOPS[dtype], 4)), tflops, gbs
-    return dict(bound="hbm", achieved=round(gbs, 1), peak=PEAK_HBM_GBS, unit="GB/s",
-                frac=round(gbs / PEAK_HBM_GBS, 4)), tflops, gbs
-
-
-def time_large_f16(dev, steps, warmup):
-    """Large float16 contractions (float32 output): the north star's
-    "large fp16 contractions" on the dense float16 MFMA roof, with torch's
-    matmul (the vendor library, float16 output) timed beside them."""
-    import torch
-
-    from pto_einsum import EinsumBuilder
-
-    out = []
     n = 8192
     g = torch.Generator().manual_seed(77)
     x = (torch.randn(n, n, generator=g) / 64).half().to(dev)
     y = (torch.randn(n, n, generator=g) / 64).half().to(dev)
-    for eq, label in (("ij,jk->ik", "NN"), ("ik,jk->ij", "NT")):
-        r = EinsumBuilder(eq, [tuple(x.shape), tuple(y.shape)], torch.float16).build()
-        f, nb = work(eq, x, y)
-        km = time_graph(r, x, y, max(5, steps // 2), max(2, warmup // 2), r(x, y).numel() * 4)
-        rf, tf, gb = roofline(f, nb, km, "f16")
-        out.append(dict(shape=f"{n}^3 {label}", equation=eq, dtype="f16", us=round(km * 1e3, 1),
-                        tflops=round(tf, 1), roof=rf["bound"], frac=rf["frac"]))
-        log(f"bench: large f16 {eq} {km * 1e3:.1f} us {tf:.1f} TFLOP/s ({rf['frac'] * 100:.1f}% of fp16 MFMA)")
-        del r
-        torch.cuda.empty_cache()
-    yt = y.t().contiguous()
-    for label, fn in (("NN", lambda: torch.matmul(x, y)), ("NT", lambda: torch.matmul(x, yt.t()))):
-        for _ in range(3):
-            fn()
+    out = []
+    for label in ("NN", "NT"):
+        yy = y if label == "NN" else y.t().contiguous()
+        sets = replicate((x, yy), 2)
+        fn = (lambda a, b: torch.matmul(a, b)) if label == "NN" else (lambda a, b: torch.matmul(a, b.t()))
+        for i in range(3):
+            fn(*sets[i % 2])
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
-        for _ in range(10):
-            fn()
+        for i in range(10):
+            fn(*sets[i % 2])
         e1.record()
         torch.cuda.synchronize()
         t = e0.elapsed_time(e1) / 10
@@ -476,22 +612,24 @@ def time_large_f16(dev, steps, warmup):
                         us=round(t * 1e3, 1), tflops=round(tf, 1), roof="mfma",
                         frac=round(tf / PEAK_TFLOPS["f16"], 4)))
         log(f"bench: torch.matmul f16 {label} {t * 1e3:.1f} us {tf:.1f} TFLOP/s")
-    del x, y, yt
+        del sets
+    del x, y
     torch.cuda.empty_cache()
     return out
 
 
-def cpu_baseline(nbatch, budget_s=10.0, max_reps=30):
-    """Reference CPU route on `nbatch` of config 2's 16 batches, 1 thread,
-    called repeatedly for about `budget_s` seconds (median call time)."""
-    import numpy as np
+# ------------------------------------------------------------ CPU baseline --
+
+def cpu_baseline(budget_s=10.0):
+    """Reference CPU route on the whole of config 2 (all 16 batches), one
+    thread: called until `budget_s` is spent (at least once); best call."""
     import torch
 
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
     import ref_build
 
-    eq, s0, s1 = "bji,bjk->bik", (nbatch, 777, 1000), (nbatch, 777, 1536)
+    eq, s0, s1 = "bji,bjk->bik", (16, 777, 1000), (16, 777, 1536)
     g = torch.Generator().manual_seed(1)
     a = torch.randn(s0, generator=g).numpy()
     b = torch.randn(s1, generator=g).numpy()
@@ -503,18 +641,20 @@ def cpu_baseline(nbatch, budget_s=10.0, max_reps=30):
         fn = lambda: oracle.einsum(eq, a, b)  # noqa: E731
     times = []
     t_start = time.perf_counter()
-    while len(times) < max_reps and (time.perf_counter() - t_start) < budget_s:
+    while not times or (time.perf_counter() - t_start) + statistics.median(times) < budget_s:
         t = time.perf_counter()
         fn()
         times.append(time.perf_counter() - t)
-    dt = statistics.median(times)
-    flops = 2.0 * nbatch * 1000 * 1536 * 777
+    dt = min(times)
+    flops = 2.0 * 16 * 1000 * 1536 * 777
     return dict(value=round(flops / dt / 1e12, 6), unit="TFLOP/s", cores=1, kind=kind,
-                sample=(f"{nbatch} of 16 batches of config 2 (bji,bjk->bik float32, j=777, i=1000, "
-                        f"k=1536), {flops / 1e9:.2f} GFLOP per call, called {len(times)} times "
-                        f"({sum(times):.1f} s); median call {dt:.3f} s on 1 thread of {os.cpu_count()}"),
+                sample=(f"the whole of config 2 (bji,bjk->bik float32, b=16, j=777, i=1000, k=1536), "
+                        f"{flops / 1e9:.1f} GFLOP per call, {len(times)} call(s) in {sum(times):.1f} s; "
+                        f"best call {dt:.2f} s on 1 thread of {os.cpu_count()}"),
                 seconds=round(sum(times), 3))
 
+
+# -------------------------------------------------------------------- main --
 
 def main():
     args = parse()
@@ -525,8 +665,12 @@ def main():
         sys.exit(2)
     import torch
 
-    from pto_einsum import EinsumBuilder
-
+    groups = all_cases()
+    if args.list_cases:
+        for grp, cases in groups.items():
+            for c in cases:
+                print(f"{grp}: {c.name}")
+        return
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     if args.copy_probe:
         copy_probe()
@@ -534,59 +678,52 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
 
-    # ---- headline: config 2 ----
-    eq, s0, s1 = "bji,bjk->bik", (16, 777, 1000), (16, 777, 1536)
-    g = torch.Generator().manual_seed(2)
-    a = torch.randn(s0, generator=g).to(dev)
-    b = torch.randn(s1, generator=g).to(dev)
-    log(f"bench: building {eq} {s0} x {s1} float32")
-    builder = EinsumBuilder(eq, [s0, s1], torch.float32)
-    run = builder.build()
-    log(f"bench: plan {builder.launch_plan.gemm} staged={builder.launch_plan.gather0 or builder.launch_plan.gather1 or builder.launch_plan.scatter_out}")
-    per, total_ms = time_runner(run, a, b, args.steps, args.warmup)
+    if args.profile:
+        found = [c for cs in groups.values() for c in cs if c.name == args.profile]
+        if not found:
+            sys.exit(f"bench.py: no case {args.profile!r} (see --list-cases)")
+        measure(found[0], dev, args.steps, args.warmup, profile_calls=max(1, args.steps))
+        print(json.dumps({"profiled": args.profile, "calls": max(1, args.steps)}))
+        return
+
+    # ---- headline: config 2, rotated operand sets ----
+    head = groups["headline"][0]
+    call, operands, set_bytes = head.prepare(dev)
+    nsets = n_sets(set_bytes)
+    sets = replicate(operands, nsets)
+    a, b = operands
+    eq = "bji,bjk->bik"
+    log(f"bench: config 2 {eq} {tuple(a.shape)} x {tuple(b.shape)} float32, {nsets} rotated operand sets")
+    per, total_ms = time_runner(call, sets, args.steps, args.warmup)
     flops, nbytes = work(eq, a, b)
     ms_per_step = total_ms / args.steps
     kernel_ms = statistics.mean(per)
     roof, _, _ = roofline(flops, nbytes, kernel_ms, "f32")
-    roof["traffic"] = traffic_from_profile()
+    roof["traffic"], roof["traffic_source"] = traffic_from_profile()
+    roof["kernel_us"] = round(kernel_ms * 1e3, 2)
     value = flops / (ms_per_step * 1e-3) / 1e12
     log(f"bench: config 2 {ms_per_step * 1e3:.1f} us/step, kernel {kernel_ms * 1e3:.1f} us, {value:.2f} TFLOP/s")
+    del sets, operands, call
+    torch.cuda.empty_cache()
 
-    per_config = []
+    rows = {k: [] for k in groups if k != "headline"}
     if not args.no_configs:
-        for name, ceq, gen, dt in config_list():
-            gg = torch.Generator().manual_seed(100 + len(per_config))
-            x, y = gen(gg)
-            x, y = x.to(dev), y.to(dev)
-            r = EinsumBuilder(ceq, [tuple(x.shape), tuple(y.shape)], x.dtype).build()
-            f, nb = work(ceq, x, y)
-            km = time_graph(r, x, y, max(10, args.steps), max(3, args.warmup // 2),
-                            r(x, y).numel() * 4)
-            rf, tf, gb = roofline(f, nb, km, dt)
-            per_config.append(dict(config=name, equation=ceq, dtype=dt, us=round(km * 1e3, 2),
-                                   tflops=round(tf, 3), gbs=round(gb, 1), roof=rf["bound"],
-                                   frac=rf["frac"]))
-            log(f"bench: config {name} {ceq} {km * 1e3:.1f} us  {tf:.2f} TFLOP/s  {gb:.0f} GB/s  "
-                f"{rf['bound']} {rf['frac'] * 100:.1f}%")
-            del x, y, r
-            torch.cuda.empty_cache()
+        for grp in ("per_config", "transposes", "large_f16", "gdn"):
+            for case in groups[grp]:
+                rows[grp].append(measure(case, dev, args.steps, args.warmup))
+        pc = rows["per_config"]
+        chain = sum(c["us"] for c in pc if c["config"] in ("5.1", "5.2", "5.3"))
+        for c in pc:
+            if c["config"].startswith("5.F"):
+                c["three_einsums_us"] = round(chain, 2)
+        rows["large_f16"] += time_torch_matmul(dev)
+        rows["gdn_stages"] = time_gdn_stages(dev, args.steps)
 
-    if not args.no_configs:
-        fused = time_fused_chain(dev, args.steps, args.warmup)
-        chain_us = sum(c["us"] for c in per_config if c["config"] in ("5.1", "5.2", "5.3"))
-        fused["three_einsums_us"] = round(chain_us, 2)
-        per_config.append(fused)
-        log(f"bench: config 5 fused tn,sn,sp,ts->tp {fused['us']:.1f} us ({fused['tflops']:.1f} TFLOP/s "
-            f"dense-equivalent, {fused['roof']} {fused['frac'] * 100:.1f}%; float32 P.V {fused['precise_us']:.1f} us); "
-            f"the three einsums take {chain_us:.1f} us")
-
-    transposes = [] if args.no_configs else time_transposes(dev, args.steps, args.warmup)
-    large_f16 = [] if args.no_configs else time_large_f16(dev, args.steps, args.warmup)
-    gdn, gdn_stages = ([], []) if args.no_configs else time_gdn(dev, args.steps, args.warmup)
-
-    log("bench: timing the CPU baseline")
-    cpu = cpu_baseline(args.cpu_sample_batches, args.cpu_seconds)
-    log(f"bench: cpu baseline {cpu}")
+    cpu = None
+    if not args.no_cpu:
+        log("bench: timing the CPU baseline")
+        cpu = cpu_baseline(args.cpu_seconds)
+        log(f"bench: cpu baseline {cpu}")
 
     line = {
         "metric": "einsum TFLOP/s & HBM GB/s as % of MI355X roofline, per equation",
@@ -600,17 +737,14 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (seeded standard-normal operands, resident in HBM)",
+        "data": (f"synthetic (seeded standard-normal operands, resident in HBM; {nsets} operand sets "
+                 f"rotated per step, >= 1 GiB, so no step reads the Infinity Cache's copy)"),
         "config": {"workload": "config 2: bji,bjk->bik float32 b=16 i=1000 j=777 k=1536",
-                   "equation": eq, "shapes": [list(s0), list(s1)], "parallelism": "single GPU"},
+                   "equation": eq, "shapes": [list(a.shape), list(b.shape)], "parallelism": "single GPU"},
         "roofline": roof,
         "cpu_baseline": cpu,
-        "per_config": per_config,
-        "transposes": transposes,
-        "large_f16": large_f16,
-        "gdn": gdn,
-        "gdn_stages": gdn_stages,
     }
+    line.update(rows)
     print(json.dumps(line), flush=True)
 
 

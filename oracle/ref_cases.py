@@ -13,8 +13,8 @@ exactly the routes the reference exercises:
   tests/test_llm_ops.py:81-107 at T=S in {96, 320};
 * ``CONFIG_CASES``     -- the BASELINE equations at reduced sizes, plus edge
   shapes (size-1 axes, scalar output, multi-axis contraction order);
-* ``BENCH_SAMPLE``     -- the bounded CPU-baseline sample bench.py times:
-  one batch of config 2 (``bji,bjk->bik``, j=777, i=1000, k=1536).
+* ``BENCH_SAMPLE``     -- the CPU baseline bench.py times: the whole of
+  config 2 (``bji,bjk->bik``, b=16, j=777, i=1000, k=1536).
 """
 
 EINSUM_CASES = [
@@ -127,7 +127,7 @@ CONFIG_CASES = [
     ("xyz,zyw->wx", (3, 4, 5), (5, 4, 6)),
 ]
 
-BENCH_SAMPLE = ("bji,bjk->bik", (1, 777, 1000), (1, 777, 1536))
+BENCH_SAMPLE = ("bji,bjk->bik", (16, 777, 1000), (16, 777, 1536))
 
 REF_CASES = (EINSUM_CASES + ATTENTION_CASES + BROADCAST_CASES + CHAIN_CASES
              + CONFIG_CASES + [BENCH_SAMPLE])
