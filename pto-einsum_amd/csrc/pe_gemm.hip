@@ -35,6 +35,12 @@
 #define PE_GEMM_BIG_MIN_FILL 0.95
 #endif
 
+// float16 GEMMs bound by matrix-core issue take 256x256 tiles (pe_gemm_big.h)
+// when those fill at least one round of CUs.
+#ifndef PE_GEMM_BIG_F16
+#define PE_GEMM_BIG_F16 1
+#endif
+
 namespace pe {
 
 // Deterministic split reduction.  Each thread owns VEC consecutive outputs
@@ -143,6 +149,47 @@ bool hbm_bound(const pe_gemm_desc& d) {
     const double flops = 2.0 * nb * double(d.M) * d.N * d.K;
     const double peak = d.dtype == PE_F32 ? 157.3e12 : 2516.6e12;
     return bytes / 8.0e12 > flops / peak;
+}
+
+// The 256x256 float16 kernel: for direct-load float16 operands of GEMMs
+// whose MFMA work outweighs their compulsory traffic, when its tiles fill at
+// least one round of CUs (one block per CU) and cover no more padding than
+// 128x128 tiles would.  tile == 1 asks for it explicitly.
+bool big_f16(const pe_gemm_desc& d, bool dl, int al, int bl) {
+    if (!PE_GEMM_BIG_F16 || d.dtype != PE_F16 || !dl || d.split_k > 1) return false;
+    if (gemm_big_resident(al, bl) < 1) return false;
+    if (d.tile == 1) return true;
+    if (d.tile != 0 || d.split_k != 0 || hbm_bound(d) || d.K < 128) return false;
+    const int64_t tm = ceil_div(d.M, 256), tn = ceil_div(d.N, 256);
+    if (batch_total(d) * tm * tn < cu_count()) return false;
+    return tm * 256 * tn * 256 <= ceil_div(d.M, 128) * 128 * ceil_div(d.N, 128) * 128;
+}
+
+// The descriptor with adjacent batch axes merged where all three operands
+// address them as one axis (outer stride = inner extent x inner stride);
+// extent-1 axes are dropped.
+pe_gemm_desc merged_batch(const pe_gemm_desc& d) {
+    pe_gemm_desc m = d;
+    m.nbatch = 0;
+    for (int i = 0; i < d.nbatch; ++i) {
+        if (d.batch_shape[i] == 1) continue;
+        const int k = m.nbatch - 1;
+        if (k >= 0 && m.a_bstride[k] == d.batch_shape[i] * d.a_bstride[i] &&
+            m.b_bstride[k] == d.batch_shape[i] * d.b_bstride[i] &&
+            m.c_bstride[k] == d.batch_shape[i] * d.c_bstride[i]) {
+            m.batch_shape[k] *= d.batch_shape[i];
+            m.a_bstride[k] = d.a_bstride[i];
+            m.b_bstride[k] = d.b_bstride[i];
+            m.c_bstride[k] = d.c_bstride[i];
+            continue;
+        }
+        m.batch_shape[m.nbatch] = d.batch_shape[i];
+        m.a_bstride[m.nbatch] = d.a_bstride[i];
+        m.b_bstride[m.nbatch] = d.b_bstride[i];
+        m.c_bstride[m.nbatch] = d.c_bstride[i];
+        ++m.nbatch;
+    }
+    return m;
 }
 
 // Orientation of a 256-wide tile: along the longer output axis; for equal
@@ -309,8 +356,10 @@ int validate_gemm(const pe_gemm_desc& d) {
     if (d.dtype != PE_F32 && d.dtype != PE_F16)
         return fail(PE_ERR_UNSUPPORTED, "gemm: dtype must be PE_F32 or PE_F16");
     if (d.nbatch < 0 || d.nbatch > PE_MAX_DIMS) return fail(PE_ERR_INVALID, "gemm: nbatch out of range");
-    if (d.tile != 0 && d.tile != 64 && d.tile != 128 && d.tile != 192 && d.tile != 256)
-        return fail(PE_ERR_INVALID, "gemm: tile must be 0, 64, 128, 192 or 256");
+    if (d.tile != 0 && d.tile != 1 && d.tile != 64 && d.tile != 128 && d.tile != 192 && d.tile != 256)
+        return fail(PE_ERR_INVALID, "gemm: tile must be 0, 1, 64, 128, 192 or 256");
+    if (d.tile == 1 && (d.dtype != PE_F16 || d.split_k > 1))
+        return fail(PE_ERR_UNSUPPORTED, "gemm: the 256x256 tile (1) is float16 only, without a K split");
     if (d.tile == 192 && d.dtype != PE_F32)
         return fail(PE_ERR_UNSUPPORTED, "gemm: the 192 tile is float32 only");
     if (d.split_k < 0) return fail(PE_ERR_INVALID, "gemm: split_k must be >= 0");
@@ -387,6 +436,34 @@ extern "C" int pe_gemm(const pe_gemm_desc* d, const void* a, const void* b, floa
     const int al = classify(d->M, d->K, d->a_ms, d->a_ks, d->a_bstride, d->nbatch, a, vec);
     const int bl = classify(d->N, d->K, d->b_ns, d->b_ks, d->b_bstride, d->nbatch, b, vec);
     bool dl = d->tile != 192 && gemm_dl_eligible(d->dtype, al, bl, d->M, d->N, d->K, d->c_ms, d->c_ns);
+    if (big_f16(*d, dl, al, bl) && merged_batch(*d).nbatch <= 1) {
+        const pe_gemm_desc md = merged_batch(*d);
+        GemmArgs g{};
+        g.a = a; g.b = b; g.c = c;
+        g.partial = nullptr;
+        g.M = int32_t(d->M); g.N = int32_t(d->N); g.K = int32_t(d->K);
+        g.nsplit = 1;
+        g.k_per_split = int32_t(d->K);
+        g.tiles_m = int32_t(ceil_div(d->M, 256));
+        g.tiles_n = int32_t(ceil_div(d->N, 256));
+        g.tiles_per_batch = uint32_t(g.tiles_m) * uint32_t(g.tiles_n);
+        g.nbatch_total = uint32_t(nb);
+        g.total_blocks = g.tiles_per_batch * g.nbatch_total;
+        g.grid = g.total_blocks;
+        g.store_nt = nb * d->M * d->N * 4 >= PE_NT_MIN_BYTES;
+        g.a_ms = d->a_ms; g.a_ks = d->a_ks; g.b_ks = d->b_ks; g.b_ns = d->b_ns;
+        g.c_ms = d->c_ms; g.c_ns = d->c_ns;
+        g.nbatch = md.nbatch;
+        g.batch_div[0].init(uint32_t(md.nbatch ? md.batch_shape[0] : 1));
+        g.a_bs[0] = md.nbatch ? md.a_bstride[0] : 0;
+        g.b_bs[0] = md.nbatch ? md.b_bstride[0] : 0;
+        g.c_bs[0] = md.nbatch ? md.c_bstride[0] : 0;
+        PE_CHECK_HIP(launch_gemm_big(al, bl, g, s));
+        return PE_OK;
+    }
+    if (d->tile == 1)
+        return fail(PE_ERR_UNSUPPORTED,
+                    "gemm: the 256x256 tile needs 16-byte vector operands and batch axes that merge into one");
     GemmChoice ch = choose(*d, dl, al, bl);
     if (dl && gemm_dl_resident(d->dtype, ch.bm, ch.bn, ch.minb, al, bl) < 1) {
         // the chosen direct-load instantiation spills: the staged kernel

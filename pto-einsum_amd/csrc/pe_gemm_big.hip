@@ -1,0 +1,41 @@
+// Host side of the large float16 GEMM (pe_gemm_big.h): instantiations for
+// the four operand layout pairings, their residency (with the spill check)
+// and the persistent launch, one block per CU.
+#include "pe_gemm_big.h"
+
+namespace pe {
+
+static const void* big_kernel(int al, int bl) {
+    if (al == L_K)
+        return bl == L_K ? reinterpret_cast<const void*>(&gemm_big_kernel<L_K, L_K>)
+                         : reinterpret_cast<const void*>(&gemm_big_kernel<L_K, L_MN>);
+    return bl == L_K ? reinterpret_cast<const void*>(&gemm_big_kernel<L_MN, L_K>)
+                     : reinterpret_cast<const void*>(&gemm_big_kernel<L_MN, L_MN>);
+}
+
+int gemm_big_resident(int al, int bl) {
+    static int cache[4] = {-1, -1, -1, -1};
+    int& c = cache[(al == L_K) * 2 + (bl == L_K)];
+    if (c < 0) {
+        hipFuncAttributes at{};
+        int n = 0;
+        const void* k = big_kernel(al, bl);
+        if (hipFuncGetAttributes(&at, k) != hipSuccess || at.localSizeBytes > 16 ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k, kGemmThreads, 0) != hipSuccess || n < 1)
+            n = 0;
+        c = n;
+    }
+    return c;
+}
+
+hipError_t launch_gemm_big(int al, int bl, const GemmArgs& g, hipStream_t s) {
+    const int resident = gemm_big_resident(al, bl);
+    if (resident < 1) return hipErrorInvalidConfiguration;
+    GemmArgs a = g;
+    const uint32_t cap = uint32_t(cu_count()) * uint32_t(resident);
+    if (a.grid > cap) a.grid = cap;
+    void* args[] = {&a};
+    return hipLaunchKernel(big_kernel(al, bl), dim3(a.grid), dim3(kGemmThreads), args, 0, s);
+}
+
+}  // namespace pe
