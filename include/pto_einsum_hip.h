@@ -175,6 +175,10 @@ int pe_reduce_axes(const pe_reduce_desc* d, const void* src, float* dst, void* s
 /* Plan executor: the body of every per-shape run_einsum_exec. */
 int pe_einsum_exec(const pe_einsum_plan* p, const void* in0, const void* in1, float* out,
                    void* ws, void* stream);
+/* Workspace bytes a plan needs (>= 256): what pe_einsum_setup allocates, for
+ * callers that provide the workspace themselves (no counterpart in the
+ * reference, whose setup always allocates). */
+int64_t pe_einsum_workspace_bytes(const pe_einsum_plan* p);
 /* Allocates the plan's workspace (>= 256 bytes, never NULL on success). */
 void* pe_einsum_setup(const pe_einsum_plan* p, void* stream);
 /* Waits for the device, then frees a workspace from pe_einsum_setup. */

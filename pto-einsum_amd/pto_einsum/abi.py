@@ -130,6 +130,8 @@ def bind(lib=None):
     lib.pe_gemm_workspace_bytes.argtypes = [ctypes.POINTER(GemmDesc)]
     lib.pe_gemm_workspace_bytes.restype = ctypes.c_int64
     lib.pe_einsum_exec.argtypes = [ctypes.POINTER(EinsumPlan), vp, vp, vp, vp, vp]
+    lib.pe_einsum_workspace_bytes.argtypes = [ctypes.POINTER(EinsumPlan)]
+    lib.pe_einsum_workspace_bytes.restype = ctypes.c_int64
     lib.pe_einsum_setup.argtypes = [ctypes.POINTER(EinsumPlan), vp]
     lib.pe_einsum_setup.restype = vp
     lib.pe_einsum_teardown.argtypes = [vp]

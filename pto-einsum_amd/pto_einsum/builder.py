@@ -62,7 +62,7 @@ class EinsumBuilder:
         self.code_hash: Optional[str] = None
         self.target_dir: Optional[str] = None
         self.launch_plan: Optional[launch.LaunchPlan] = None
-        self._workspaces: Dict[int, int] = {}
+        self._workspaces: Dict[int, tuple] = {}   # device -> (workspace tensor, its allocation stream)
         self._swap_operands = False
         self._exec_shapes = tuple(tuple(s) for s in input_shapes)
         self._exec_equation: Optional[str] = None
@@ -155,19 +155,11 @@ class EinsumBuilder:
 
     # --- lifecycle (builder.py:738-759) ----------------------------------
     def _free_workspaces(self):
-        if self.lib is None or self._route_device == "cpu":
-            self._workspaces = {}
-            return
-        for ws in self._workspaces.values():
-            self.lib.run_einsum_teardown(ws)
+        # The runner's workspaces are torch allocations: dropping them returns
+        # the memory to torch's stream-ordered caching allocator, which hands
+        # it out again only behind the work already queued on the streams
+        # that used it (recorded in run()).  No device synchronisation.
         self._workspaces = {}
-
-    def __del__(self):
-        try:
-            if getattr(self, "_workspaces", None) and getattr(self, "lib", None) is not None:
-                self._free_workspaces()
-        except Exception:
-            pass
 
     def cleanup(self):
         self._free_workspaces()
@@ -185,6 +177,10 @@ class EinsumBuilder:
         self.compile()
         self.load_library()
         gpu = self._route_device != "cpu"
+        if gpu:
+            from . import abi
+
+            self._ws_bytes = int(abi.bind().pe_einsum_workspace_bytes(ctypes.byref(abi.einsum_plan(self.launch_plan))))
 
         def run(*operands):
             if len(operands) != 2:
@@ -221,14 +217,21 @@ class EinsumBuilder:
                 out = torch.empty(out_shape, dtype=torch.float32, device=dev)
                 stream = runtime.current_stream_ptr(dev)
                 idx = dev.index if dev.index is not None else torch.cuda.current_device()
-                ws = self._workspaces.get(idx)
-                if ws is None:
-                    ws = self.lib.run_einsum_setup(stream)
-                    if not ws:
-                        raise RuntimeError(f"run_einsum_setup failed: {runtime.last_error()}")
-                    self._workspaces[idx] = ws
+                # Workspace (split-K partials, staged operands): a torch
+                # allocation per device, so creating it is stream-ordered and
+                # allowed under graph capture, and dropping it needs no
+                # synchronisation.  A use on another stream than the one it
+                # was allocated on is recorded, so the allocator does not
+                # reuse the memory before that stream's work is done.
+                entry = self._workspaces.get(idx)
+                if entry is None:
+                    entry = (torch.empty(self._ws_bytes, dtype=torch.uint8, device=dev), stream)
+                    self._workspaces[idx] = entry
+                elif entry[1] != stream:
+                    entry[0].record_stream(torch.cuda.current_stream(dev))
                 rc = self.lib.run_einsum_exec(self._ptr(inp0, self.c_type), self._ptr(inp1, self.c_type),
-                                              self._ptr(out, ctypes.c_float), ws, stream)
+                                              self._ptr(out, ctypes.c_float), ctypes.c_void_p(entry[0].data_ptr()),
+                                              stream)
                 runtime.check(rc, "run_einsum_exec")
             return out
 
@@ -238,6 +241,10 @@ class EinsumBuilder:
 _RUNNER_CACHE_SIZE = 64
 _runners: "collections.OrderedDict" = collections.OrderedDict()
 _runners_lock = threading.Lock()
+# Runners handed out while a StageGraph captures: the graph keeps them (and so
+# their workspaces, which its replays read and write) alive after the cache
+# evicts them.  None outside a capture.
+_capture_pins: Optional[list] = None
 
 
 def _reduce_operand(x: torch.Tensor, subs: str, solo: str) -> torch.Tensor:
@@ -316,9 +323,23 @@ def einsum(equation: str, *operands, device: str = "cuda", reduce_solo_axes: boo
         entry = (builder, builder.build())
         with _runners_lock:
             _runners[key] = entry
+    with _runners_lock:
+        # No eviction while a graph is being captured: a runner used earlier
+        # in the capture must keep its workspace, which the graph reads at
+        # every replay.  The cache shrinks back at the first call after it.
+        if len(_runners) > _RUNNER_CACHE_SIZE and not _capturing():
             while len(_runners) > _RUNNER_CACHE_SIZE:
                 _runners.popitem(last=False)
+        if _capture_pins is not None:
+            _capture_pins.append(entry)
     return entry[1](inp0, inp1)
+
+
+def _capturing() -> bool:
+    try:
+        return torch.cuda.is_available() and torch.cuda.is_current_stream_capturing()
+    except Exception:
+        return False
 
 
 def clear_runner_cache():

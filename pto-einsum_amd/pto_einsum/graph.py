@@ -17,15 +17,19 @@ The library's execution entry points are safe to capture: they launch kernels
 on the caller's current stream and never allocate device memory, synchronise,
 or clear memory with a memset (split-K partial sums are combined by a
 reduction kernel in a fixed order), so every replay is bit-identical to an
-eager call on the same inputs.  What must not run under capture -- building a
-runner, creating its per-device workspace -- happens in the eager warm-up
-calls that precede the capture.
+eager call on the same inputs.  Runner workspaces are torch allocations
+(allowed under capture); the graph keeps every einsum runner it captured alive,
+so their workspaces outlive evictions from the runner cache, which pauses
+while a capture runs.  Building runners (host-side code generation) is best
+left to the eager warm-up calls that precede the capture.
 """
 from __future__ import annotations
 
 from typing import Any, Callable
 
 import torch
+
+from . import builder
 
 
 class StageGraph:
@@ -50,8 +54,17 @@ class StageGraph:
             torch.cuda.current_stream().wait_stream(side)
             torch.cuda.synchronize()
             self._graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(self._graph):
-                self.outputs = fn()
+            # Every einsum runner used in the capture is kept with the graph:
+            # its workspace is part of what the replays read and write, so it
+            # must outlive the runner cache's eviction of that runner.
+            prev = builder._capture_pins
+            builder._capture_pins = []
+            try:
+                with torch.cuda.graph(self._graph):
+                    self.outputs = fn()
+            finally:
+                self._pinned = builder._capture_pins
+                builder._capture_pins = prev
             torch.cuda.synchronize()
 
     def replay(self):
