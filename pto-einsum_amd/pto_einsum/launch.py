@@ -133,6 +133,37 @@ def _candidate_orders(group: Sequence[str], size, strides: Sequence[Dict[str, in
     return seen
 
 
+# Smallest extent a free group keeps when its other axes become batch axes.
+kMinKeptFree = 16
+
+
+def _group_order(group: Sequence[str], size, strides: Sequence[Dict[str, int]]):
+    """An order of ``group`` that addresses like one axis in every tensor of
+    ``strides``, or None."""
+    for cand in _candidate_orders(list(group), size, strides):
+        if all(_mergeable(cand, size, st) for st in strides):
+            return cand
+    return None
+
+
+def _largest_collapsing_subset(group: Sequence[str], size, strides: Sequence[Dict[str, int]], required: str):
+    """The subset of ``group`` holding ``required`` with the largest extent
+    that collapses in every tensor of ``strides`` (ordered as it collapses),
+    or None."""
+    from itertools import combinations
+
+    best, best_ext = None, 0
+    for r in range(len(group) - 1, 0, -1):
+        for sub in combinations(group, r):
+            if required not in sub:
+                continue
+            order = _group_order(sub, size, strides)
+            ext = prod(size[a] for a in sub)
+            if order is not None and ext > best_ext:
+                best, best_ext = order, ext
+    return best
+
+
 def _component_descs(plan: LaunchPlan, recipe: Dict, shape0, shape1, dtype_code: int, elem: int):
     """Descriptors of the staged component entry points: the operand
     permutations into ``[I, L0, C]`` / ``[I, C, L1]``, the canonical batched
@@ -195,6 +226,24 @@ def plan_launch(recipe: Dict, exec_eq: str, shape0, shape1, dtype_code: int) -> 
     mgrp = list(roles["invariant0"])
     ngrp = list(roles["invariant1"])
     kgrp = list(roles["contract"])
+    # A free group (M or N) that collapses to one stride in neither order of
+    # its two tensors keeps its largest subset that does and hands the other
+    # axes to the batch: e.g. abc,cd->adb runs as a batch over a of
+    # (b, c) x (c, d) GEMMs storing straight into the output, one launch and
+    # no workspace.  (A free axis made batch has stride 0 in the tensor that
+    # lacks it.)  The kept subset holds the group's axis that is innermost in
+    # the output, so the fused store stays coalesced.  Only when no such
+    # subset reaches kMinKeptFree elements does the tensor that breaks the
+    # group go through the workspace instead.
+    for grp, tensors in ((mgrp, (st0, sto)), (ngrp, (st1, sto))):
+        if len(grp) < 2 or _group_order(grp, size, tensors) is not None:
+            continue
+        inner = min((a for a in grp if size[a] != 1), key=lambda a: sto[a], default=grp[-1])
+        kept = _largest_collapsing_subset(grp, size, tensors, inner)
+        if kept is not None and prod(size[a] for a in kept) >= kMinKeptFree:
+            moved = [a for a in grp if a not in kept]
+            grp[:] = list(kept)
+            batch += moved
     I, L0, L1 = prod(size[a] for a in batch), prod(size[a] for a in mgrp), prod(size[a] for a in ngrp)
 
     # Staging: a tensor in which some axis group does not collapse is staged
@@ -252,7 +301,10 @@ def plan_launch(recipe: Dict, exec_eq: str, shape0, shape1, dtype_code: int) -> 
         axes = [a for part in layout for a in part]
         return dict(zip(axes, row_major_strides([size[a] for a in axes])))
 
-    layouts = {"A": (border, orders["M"], orders["K"]), "B": (border, orders["K"], orders["N"]),
+    # (Batch axes a staged tensor does not carry -- free axes made batch --
+    # are left out of its layout.)
+    layouts = {"A": ([a for a in border if a in t0], orders["M"], orders["K"]),
+               "B": ([a for a in border if a in t1], orders["K"], orders["N"]),
                "C": (border, orders["M"], orders["N"])}
     stage_st = {t: staged_strides(layouts[t]) for t in layouts}
 
@@ -265,14 +317,15 @@ def plan_launch(recipe: Dict, exec_eq: str, shape0, shape1, dtype_code: int) -> 
     bax = [a for a in sorted(batch, key=to.index) if size[a] != 1]
     bshape, ba, bb, bc = [], [], [], []
     for a in bax:
-        if bshape and ba[-1] == size[a] * sA[a] and bb[-1] == size[a] * sB[a] and bc[-1] == size[a] * sC[a]:
+        xa, xb, xc = sA.get(a, 0), sB.get(a, 0), sC[a]
+        if bshape and ba[-1] == size[a] * xa and bb[-1] == size[a] * xb and bc[-1] == size[a] * xc:
             bshape[-1] *= size[a]
-            ba[-1], bb[-1], bc[-1] = sA[a], sB[a], sC[a]
+            ba[-1], bb[-1], bc[-1] = xa, xb, xc
         else:
             bshape.append(size[a])
-            ba.append(sA[a])
-            bb.append(sB[a])
-            bc.append(sC[a])
+            ba.append(xa)
+            bb.append(xb)
+            bc.append(xc)
     if len(bshape) > MAX_DIMS:
         raise ValueError(f"einsum '{exec_eq}': more than {MAX_DIMS} independent batch axes")
 

@@ -147,7 +147,7 @@ def test_noalloc_rejects_oversized_plan_without_launch():
     """The allocation-free executor refuses a plan whose workspace exceeds its
     static scratch, before any device call (so this runs without a GPU)."""
     lib = abi.bind()
-    b = EinsumBuilder("abc,cd->adb", [(512, 512, 64), (64, 512)], torch.float32)
+    b = EinsumBuilder("abc,cd->adb", [(1024, 8, 64), (64, 4096)], torch.float32)
     b.parse_equation()
     b.generate_code()
     assert b.launch_plan.scatter_out and b.launch_plan.ws_bytes > (64 << 20)

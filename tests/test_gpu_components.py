@@ -112,6 +112,28 @@ def test_staged_plans_on_gpu(eq, s0, s1, dtype, build_dir):
     check(got, want, contraction_size(eq, s0, s1) <= 1, RTOL[dtype], eq)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16], ids=["f32", "f16"])
+@pytest.mark.parametrize("eq,s0,s1", [("abc,cd->adb", (64, 48, 96), (96, 80)),
+                                      ("acb,cd->abd", (48, 64, 40), (64, 72)),
+                                      ("abcd,de->aebc", (4, 5, 40, 8), (8, 24)),
+                                      ("bac,cdb->adb", (3, 40, 72), (72, 20, 3))])
+def test_free_axes_made_batch_on_gpu(eq, s0, s1, dtype, build_dir):
+    """Free groups that collapse in neither tensor run as one batched GEMM
+    storing straight into the output (no workspace), against the oracle."""
+    from parity_util import RTOL, make_inputs
+    from pto_einsum import einsum
+
+    b = EinsumBuilder(eq, [s0, s1], dtype)
+    b.parse_equation()
+    b.generate_code()
+    lp = b.launch_plan
+    assert not (lp.gather0 or lp.gather1 or lp.scatter_out) and lp.ws_bytes == 0
+    x, y = make_inputs(eq, s0, s1, dtype)
+    got = einsum(eq, x.cuda(), y.cuda()).cpu().numpy()
+    want = oracle.einsum(eq, x.float().numpy(), y.float().numpy())
+    check(got, want, False, RTOL[dtype], eq)
+
+
 def _gemm_direct(a, b, M, N, K, a_ms, a_ks, b_ks, b_ns, dtype_code, tile=0, split_k=0, nbatch=2):
     """C[bt] = A[bt] @ B[bt] through pe_gemm with explicit strides; A and B are
     flat device buffers holding `nbatch` operands each."""

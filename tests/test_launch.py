@@ -28,6 +28,10 @@ EXTRA = [
     ("i,j->ji", (5,), (6,)),
     ("abcdefghij,abcdefghij->abcdefghij", (1, 2, 1, 2, 1, 2, 1, 2, 1, 3), (1, 2, 1, 2, 1, 2, 1, 2, 1, 3)),
     ("abc,abd->cd", (0, 3, 4), (0, 3, 5)),     # empty contraction -> zeros
+    ("abc,cd->adb", (6, 20, 7), (7, 8)),       # free0 split in the output: a made batch
+    ("acb,cd->abd", (5, 7, 18), (7, 8)),       # ... split in operand 0
+    ("abcd,de->bcea", (4, 5, 6, 8), (8, 24)),  # free0 {a,b,c}: {b,c} kept, a made batch
+    ("bac,cdb->adb", (3, 4, 7), (7, 20, 3)),   # a true batch axis beside a promoted one
 ]
 CASES = EINSUM_CASES + ATTENTION_CASES + BROADCAST_CASES + CHAIN_CASES + CONFIG_CASES + EXTRA
 
@@ -104,6 +108,10 @@ def test_plan_descriptors_compute_the_einsum(eq, s0, s1):
     ("bvhd,bvhe->bhde", (2, 128, 16, 128), (2, 128, 16, 128), (False, False, False)),  # TN
     ("bhsc,bcht->bsht", (2, 8, 16, 20), (2, 20, 8, 24), (False, False, False)),
     ("abc,cd->adb", (5, 6, 7), (7, 8), (False, False, True)),                      # free0 split in output
+    ("abc,cd->adb", (64, 48, 96), (96, 80), (False, False, False)),                # ... a made batch
+    ("abc,cd->adb", (64, 6, 96), (96, 80), (False, False, True)),                  # ... b too small to keep
+    ("acb,cd->abd", (48, 64, 40), (64, 72), (False, False, False)),                # split in operand 0
+    ("abcd,de->aebc", (4, 5, 40, 8), (8, 24), (False, False, False)),              # {b, c} kept, a batch
     ("ikj,jlk->il", (5, 6, 7), (7, 8, 6), (False, True, False)),                   # only B moves
 ])
 def test_staging_decisions(eq, s0, s1, staged):

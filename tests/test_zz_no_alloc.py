@@ -20,9 +20,9 @@ pytestmark = pytest.mark.gpu
 CASES = [
     ("ts,sp->tp", torch.float32, ((1024, 4096), (4096, 128)), ((256, 2048), (2048, 64))),
     ("tn,sn->ts", torch.float16, ((512, 8192), (256, 8192)), ((128, 1024), (96, 1024))),
-    ("abc,cd->adb", torch.float32, ((64, 48, 96), (96, 80)), ((16, 24, 40), (40, 30))),
-    ("abc,cd->adb", torch.float16, ((40, 33, 70), (70, 50)), ((9, 10, 11), (11, 12))),
-    ("acb,cd->abd", torch.float32, ((48, 64, 40), (64, 72)), ((5, 7, 6), (7, 9))),
+    ("abc,cd->adb", torch.float32, ((64, 6, 96), (96, 80)), ((16, 3, 40), (40, 30))),
+    ("abc,cd->adb", torch.float16, ((40, 9, 70), (70, 50)), ((9, 10, 11), (11, 12))),
+    ("acb,cd->abd", torch.float32, ((48, 64, 6), (64, 72)), ((5, 7, 6), (7, 9))),
     ("bji,bjk->bik", torch.float32, ((4, 300, 200), (4, 300, 260)), ((2, 37, 50), (2, 37, 41))),
     ("bsd,d->bsd", torch.float16, ((4, 256, 512), (512,)), ((2, 16, 64), (64,))),
 ]
@@ -91,8 +91,8 @@ def test_noalloc_matches_exec(eq, dtype, big, small):
 
 def test_noalloc_rejects_oversized_plan():
     lib = abi.bind()
-    # Config-3-sized staged output: far above the scratch limit.
-    b, plan = _plan("abc,cd->adb", ((512, 512, 64), (64, 512)), torch.float32)
+    # A staged output of 128 MiB: above the scratch limit.
+    b, plan = _plan("abc,cd->adb", ((1024, 8, 64), (64, 4096)), torch.float32)
     assert b.launch_plan.scatter_out
     x = torch.zeros(1, device="cuda")
     rc = lib.pe_einsum_exec_noalloc(ctypes.byref(plan), _ptr(x), _ptr(x), _ptr(x),
