@@ -154,11 +154,17 @@ int pe_linear_attention(const pe_linattn_desc* d, const void* q, const void* k, 
  * "Option A"), reached from Python through einsum(..., reduce_solo_axes=True).
  *   dst[k] = sum over r of (float)src[sum_d k_d keep_stride[d] + sum_e r_e red_stride[e]]
  * with k the row-major index over keep_shape (dst contiguous float32) and r
- * over red_shape.  Order (a function of the shapes only, so deterministic): the
- * nterm terms of an output, row-major in r, are cut into C contiguous chunks (the
- * first nterm % C one term longer); each chunk is summed from +0 and the partial
- * sums are added in chunk order from +0; C = 1 (the sequential loop) when
- * nterm <= 256 or nout >= 32768, else min(256, ceil(nterm / 256)).
+ * over red_shape.  Order (a function of the shapes, of whether the reduced axes
+ * form one stride-1 run, of 16-byte alignment and of the dtype -- never of the
+ * device -- so deterministic), with (V, L, C) as pe_reduce_order reports: the
+ * nterm terms of an output, row-major in r, form G = ceil(nterm / V) groups of V
+ * consecutive terms; the groups are cut into C contiguous chunks (the first
+ * G % C one group longer); in a chunk, lane l of L sums groups l, l + L, ...
+ * term by term from +0; the L lane sums, then the C chunk sums, are combined by
+ * a pairwise tree (for s = 1, 2, 4, ...: p[i] += p[i + s] for i a multiple of 2s
+ * with i + s in range; the result is p[0]).  An empty reduced axis gives +0.
+ * With C > 1 the call needs a workspace of pe_reduce_workspace_bytes(d) bytes
+ * (ws, ws_bytes); otherwise ws may be null.
  * nred = 0 is a conversion to float32. */
 typedef struct pe_reduce_desc {
     int32_t dtype;                      /* PE_F32 or PE_F16 */
@@ -170,7 +176,13 @@ typedef struct pe_reduce_desc {
     int64_t src_numel;
 } pe_reduce_desc;
 
-int pe_reduce_axes(const pe_reduce_desc* d, const void* src, float* dst, void* stream);
+int pe_reduce_axes(const pe_reduce_desc* d, const void* src, float* dst, void* ws, int64_t ws_bytes,
+                   void* stream);
+/* Workspace bytes pe_reduce_axes needs for d (0 when C = 1 or d is invalid). */
+int64_t pe_reduce_workspace_bytes(const pe_reduce_desc* d);
+/* The (V, L, C) of the summation order above for d and a source at src (V
+ * depends on src's 16-byte alignment), into order[0..2]. */
+int pe_reduce_order(const pe_reduce_desc* d, const void* src, int64_t* order);
 
 /* Plan executor: the body of every per-shape run_einsum_exec. */
 int pe_einsum_exec(const pe_einsum_plan* p, const void* in0, const void* in1, float* out,

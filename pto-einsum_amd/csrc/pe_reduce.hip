@@ -9,20 +9,33 @@
 // axis to reduce it converts an operand to float32 (the other operand of a
 // float16 einsum whose first operand was reduced to float32).
 //
-// Summation order, a function of (nout, nterm) only, so results are
-// deterministic and independent of the launch shape and the device:
-//   * the nterm terms of an output, in row-major order of the reduced index,
-//     are cut into C contiguous chunks, the first nterm % C of them one term
-//     longer than the rest;
-//   * each chunk is summed in order from +0, then the C partial sums are added
-//     in chunk order from +0;
-//   * C = 1 (the plain sequential loop) when nterm <= kChunkTerms or
-//     nout >= kWideOutputs, else min(kChunkThreads, ceil(nterm / kChunkTerms)).
-// C = 1 runs one thread per output (coalesced over the output axes, enough
-// threads to fill the chip); C > 1 runs one block per output, one thread per
-// chunk, for reductions with few outputs and many terms.  Both are HBM-bound;
-// the reduced index advances as an odometer (one add per term, a carry at each
-// axis wrap).
+// Summation order.  It depends on the shapes, on whether the reduced axes
+// form one contiguous run, on 16-byte alignment and on the dtype -- never on
+// the launch or the device -- so results are deterministic.  With V, L and C
+// as chosen below (pe_reduce_order reports them):
+//   * the nterm terms of an output, row-major over the reduced index, form
+//     G = ceil(nterm / V) groups of V consecutive terms (the last may be
+//     shorter);
+//   * the groups are cut into C contiguous chunks, the first G % C of them one
+//     group longer;
+//   * within a chunk, lane l of L sums the groups l, l + L, l + 2L, ... term
+//     by term in order, from +0;
+//   * the L lane sums, then the C chunk sums, are combined by a pairwise tree:
+//     for s = 1, 2, 4, ...: p[i] = p[i] + p[i + s] for i a multiple of 2s with
+//     i + s in range; the result is p[0].
+// Two layouts of the work:
+//   row mode (the reduced axes merge into one run of stride 1 with at least
+//     kRowMinTerms terms): L lanes per (output, chunk), V = 16 bytes of
+//     elements when every output's run starts 16-byte aligned, else 1; L = 64
+//     halved (down to 4) while L x kLaneGroups > G, so that short runs share
+//     a wave -- a lane reads V consecutive terms, its segment L x V;
+//   column mode (all other cases): L = V = 1, one lane per output and chunk,
+//     the 64 lanes of a wave on 64 consecutive outputs (coalesced when an
+//     output axis is the contiguous one), the terms' offsets (the same for
+//     every lane) advancing as a scalar odometer.
+// C is chosen for about kTargetWaves waves, each chunk at least a few steps
+// long; with C > 1 the chunk sums go through the caller's workspace and a
+// second kernel combines them.  Both passes are HBM-bound.
 #include "pe_common.h"
 
 #include <algorithm>
@@ -31,22 +44,30 @@
 namespace pe {
 namespace {
 
-constexpr int64_t kChunkTerms = 256;     // shortest chunk worth a thread of its own
-constexpr int64_t kWideOutputs = 32768;  // outputs enough to fill the chip one thread each
-constexpr int kChunkThreads = 256;       // chunks per output at most = block size
+constexpr int64_t kRowMinTerms = 32;    // shortest run read along the run
+constexpr int64_t kLaneGroups = 4;      // row mode: L shrinks until each lane has this many groups
+constexpr int64_t kTargetWaves = 4096;  // waves of the first pass (16 per CU)
+constexpr int64_t kMaxChunks = 4096;    // chunk sums per output (LDS of the tree pass)
 
-struct ReduceAxesArgs {
+// Load type of one group of V elements.
+template <typename T, int V> struct GroupOf { using type = T; };
+template <> struct GroupOf<float, 4> { using type = f32x4; };
+template <> struct GroupOf<_Float16, 8> { using type = f16x8; };
+
+struct RedArgs {
     const void* src;
     float* dst;
-    int64_t nout;                 // product of keep_shape
-    int64_t nterm;                // product of red_shape
-    int32_t nkeep, nred;
+    float* ws;                    // C x nout chunk sums when C > 1
+    int64_t nout, nterm;
+    int64_t G, C;                 // groups per output, chunks per output
+    int32_t L;                    // row mode: lanes per (output, chunk), a power of two <= 64
+    int32_t nkeep, nred;          // after merging
     int64_t keep_shape[PE_MAX_DIMS], keep_stride[PE_MAX_DIMS];
     int64_t red_shape[PE_MAX_DIMS], red_stride[PE_MAX_DIMS];
 };
 
 // Source offset of output element o: row-major decode over keep_shape.
-__device__ __forceinline__ int64_t keep_offset(const ReduceAxesArgs& a, int64_t o) {
+__device__ __forceinline__ int64_t keep_offset(const RedArgs& a, int64_t o) {
     int64_t rem = o, base = 0;
 #pragma unroll
     for (int d = PE_MAX_DIMS - 1; d >= 0; --d) {
@@ -59,66 +80,151 @@ __device__ __forceinline__ int64_t keep_offset(const ReduceAxesArgs& a, int64_t 
     return base;
 }
 
-// Sum of terms [t0, t1) of the output at source offset base, in order from +0.
-template <typename E>
-__device__ __forceinline__ float sum_terms(const ReduceAxesArgs& a, int64_t base, int64_t t0, int64_t t1) {
-    const auto* src = static_cast<const typename E::T*>(a.src);
-    int64_t idx[PE_MAX_DIMS];
-    int64_t off = base, rem = t0;
-#pragma unroll
-    for (int e = PE_MAX_DIMS - 1; e >= 0; --e) {
-        idx[e] = 0;
-        if (e < a.nred) {
-            const int64_t q = rem / a.red_shape[e];
-            idx[e] = rem - q * a.red_shape[e];
-            off += idx[e] * a.red_stride[e];
-            rem = q;
-        }
-    }
+__device__ __forceinline__ void chunk_range(int64_t n, int64_t C, int64_t c, int64_t& b, int64_t& e) {
+    const int64_t q = n / C, r = n % C;
+    b = c * q + (c < r ? c : r);
+    e = b + q + (c < r ? 1 : 0);
+}
+
+__device__ __forceinline__ void put(const RedArgs& a, int64_t o, int64_t c, float v) {
+    if (a.C == 1) a.dst[o] = v;
+    else a.ws[c * a.nout + o] = v;
+}
+
+// Row mode: L consecutive lanes (an aligned segment of the wave) per
+// (output, chunk); lane l of a segment sums groups l, l + L, ...
+template <typename E, int V>
+__global__ __launch_bounds__(256) void reduce_row_kernel(RedArgs a) {
+    using T = typename E::T;
+    const int L = a.L;
+    const int64_t tid = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    const int lane = int(tid & (L - 1));
+    const int64_t item = tid / L;
+    // Segments past the end stay in step (their lanes take part in the
+    // shuffles below) but read and write nothing.
+    const bool live = item < a.nout * a.C;
+    const int64_t o = live ? item / a.C : 0, c = live ? item - o * a.C : 0;
+    int64_t g0 = 0, g1 = 0;
+    if (live) chunk_range(a.G, a.C, c, g0, g1);
+    const T* p = static_cast<const T*>(a.src) + keep_offset(a, o);
     float acc = 0.0f;
-    for (int64_t t = t0; t < t1; ++t) {
-        acc = acc + E::to_f32(src[off]);
-        // Next r in row-major order: the last axis moves fastest.
+    int64_t g = g0 + lane;
+    // Whole groups, four in flight per lane (loads first, then the adds in
+    // order).
+    using Vec = typename GroupOf<T, V>::type;
+    constexpr int U = 4;
+    for (; g + (U - 1) * L < g1 && (g + (U - 1) * L + 1) * V <= a.nterm; g += U * L) {
+        Vec x[U];
 #pragma unroll
-        for (int e = PE_MAX_DIMS - 1; e >= 0; --e) {
-            if (e < a.nred) {
-                if (++idx[e] < a.red_shape[e]) {
-                    off += a.red_stride[e];
-                    break;
-                }
-                off -= (a.red_shape[e] - 1) * a.red_stride[e];
-                idx[e] = 0;
+        for (int u = 0; u < U; ++u) x[u] = *reinterpret_cast<const Vec*>(p + (g + u * L) * V);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if constexpr (V == 1) {
+                acc = acc + E::to_f32(x[u]);
+            } else {
+#pragma unroll
+                for (int v = 0; v < V; ++v) acc = acc + E::to_f32(x[u][v]);
             }
         }
     }
-    return acc;
-}
-
-template <typename E>
-__global__ __launch_bounds__(256) void reduce_axes_kernel(ReduceAxesArgs a) {
-    const int64_t step = int64_t(gridDim.x) * 256;
-    for (int64_t o = int64_t(blockIdx.x) * 256 + threadIdx.x; o < a.nout; o += step)
-        a.dst[o] = sum_terms<E>(a, keep_offset(a, o), 0, a.nterm);
-}
-
-// One block per output (grid-stride over outputs), thread c sums chunk c.
-template <typename E>
-__global__ __launch_bounds__(kChunkThreads) void reduce_axes_chunked_kernel(ReduceAxesArgs a, int32_t nchunk) {
-    __shared__ float part[kChunkThreads];
-    const int c = threadIdx.x;
-    const int64_t q = a.nterm / nchunk, r = a.nterm % nchunk;
-    const int64_t t0 = c * q + std::min<int64_t>(c, r);
-    const int64_t t1 = t0 + q + (c < r ? 1 : 0);
-    for (int64_t o = blockIdx.x; o < a.nout; o += gridDim.x) {
-        part[c] = c < nchunk ? sum_terms<E>(a, keep_offset(a, o), t0, t1) : 0.0f;
-        __syncthreads();
-        if (c == 0) {
-            float s = 0.0f;
-            for (int i = 0; i < nchunk; ++i) s = s + part[i];
-            a.dst[o] = s;
+    // Whole groups one at a time, then the last (partial) group term by term.
+    for (; g < g1 && (g + 1) * V <= a.nterm; g += L) {
+        const Vec x = *reinterpret_cast<const Vec*>(p + g * V);
+        if constexpr (V == 1) {
+            acc = acc + E::to_f32(x);
+        } else {
+#pragma unroll
+            for (int v = 0; v < V; ++v) acc = acc + E::to_f32(x[v]);
         }
-        __syncthreads();  // part[] is rewritten for the next output
     }
+    if (g < g1) {
+        for (int64_t t = g * V; t < a.nterm; ++t) acc = acc + E::to_f32(p[t]);
+    }
+    // Pairwise tree over the segment's L lanes: after the step with offset s,
+    // lane i holds the sum of the lanes of its aligned 2s block (addition is
+    // commutative, so both partners hold the same value; s < L keeps every
+    // exchange inside the segment).
+    for (int s = 1; s < L; s <<= 1) acc = acc + __shfl_xor(acc, s, 64);
+    if (live && lane == 0) put(a, o, c, acc);
+}
+
+// Column mode: one lane per (output, chunk), 64 consecutive outputs per wave.
+template <typename E>
+__global__ __launch_bounds__(256) void reduce_col_kernel(RedArgs a, int64_t ngroups) {
+    using T = typename E::T;
+    const int lane = threadIdx.x & 63;
+    const int64_t item = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (item >= ngroups * a.C) return;   // whole waves
+    const int64_t c = item / ngroups, og = item - c * ngroups;
+    const int64_t o = og * 64 + lane;
+    const bool live = o < a.nout;
+    int64_t t0, t1;
+    chunk_range(a.nterm, a.C, c, t0, t1);
+    const T* p = static_cast<const T*>(a.src) + (live ? keep_offset(a, o) : 0);
+    float acc = 0.0f;
+    if (a.nred == 1) {
+        const int64_t rs = a.red_stride[0];
+        int64_t t = t0;
+        constexpr int U = 8;
+        for (; t + U <= t1; t += U) {
+            T x[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) x[u] = live ? p[(t + u) * rs] : T(0);
+#pragma unroll
+            for (int u = 0; u < U; ++u) acc = acc + E::to_f32(x[u]);
+        }
+        for (; t < t1; ++t) acc = acc + E::to_f32(live ? p[t * rs] : T(0));
+    } else if (t1 > t0) {
+        // Odometer over the reduced axes (the same offsets for every lane).
+        int64_t idx[PE_MAX_DIMS];
+        int64_t off = 0, rem = t0;
+#pragma unroll
+        for (int e = PE_MAX_DIMS - 1; e >= 0; --e) {
+            idx[e] = 0;
+            if (e < a.nred) {
+                const int64_t q = rem / a.red_shape[e];
+                idx[e] = rem - q * a.red_shape[e];
+                off += idx[e] * a.red_stride[e];
+                rem = q;
+            }
+        }
+        for (int64_t t = t0; t < t1; ++t) {
+            acc = acc + E::to_f32(live ? p[off] : T(0));
+#pragma unroll
+            for (int e = PE_MAX_DIMS - 1; e >= 0; --e) {
+                if (e < a.nred) {
+                    if (++idx[e] < a.red_shape[e]) {
+                        off += a.red_stride[e];
+                        break;
+                    }
+                    off -= (a.red_shape[e] - 1) * a.red_stride[e];
+                    idx[e] = 0;
+                }
+            }
+        }
+    }
+    if (live) put(a, o, c, acc);
+}
+
+// Second pass: the C chunk sums of an output, combined by the pairwise tree
+// in LDS (one block per output, grid-stride over outputs).
+__global__ __launch_bounds__(256) void reduce_tree_kernel(const float* ws, float* dst, int64_t nout, int32_t C) {
+    __shared__ float buf[kMaxChunks];
+    for (int64_t o = blockIdx.x; o < nout; o += gridDim.x) {
+        for (int i = threadIdx.x; i < C; i += 256) buf[i] = ws[int64_t(i) * nout + o];
+        __syncthreads();
+        for (int s = 1; s < C; s <<= 1) {
+            for (int i = threadIdx.x * 2 * s; i < C; i += 256 * 2 * s)
+                if (i + s < C) buf[i] = buf[i] + buf[i + s];
+            __syncthreads();
+        }
+        if (threadIdx.x == 0) dst[o] = buf[0];
+        __syncthreads();  // buf is rewritten for the next output
+    }
+}
+
+__global__ __launch_bounds__(256) void zero_kernel(float* dst, int64_t n) {
+    for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += int64_t(gridDim.x) * 256) dst[i] = 0.0f;
 }
 
 int validate(const pe_reduce_desc& d) {
@@ -142,48 +248,145 @@ int validate(const pe_reduce_desc& d) {
     return PE_OK;
 }
 
+// Merges adjacent axes that address like one (outer stride = inner extent x
+// inner stride) and drops extent-1 axes; the row-major index order over the
+// axes is unchanged.
+int merge_axes(const int64_t* shape, const int64_t* stride, int n, int64_t* mshape, int64_t* mstride) {
+    int m = 0;
+    for (int i = 0; i < n; ++i) {
+        if (shape[i] == 1) continue;
+        if (m > 0 && mstride[m - 1] == shape[i] * stride[i]) {
+            mshape[m - 1] *= shape[i];
+            mstride[m - 1] = stride[i];
+        } else {
+            mshape[m] = shape[i];
+            mstride[m] = stride[i];
+            ++m;
+        }
+    }
+    return m;
+}
+
+struct RedPlan {
+    RedArgs a;
+    int mode;      // 0: zero fill (no terms), 1: row, 2: column
+    int V, L;
+    int64_t ngroups;  // column mode: waves of outputs per chunk
+};
+
+RedPlan plan_reduce(const pe_reduce_desc& d, const void* src) {
+    RedPlan p{};
+    RedArgs& a = p.a;
+    a.src = src;
+    a.nkeep = merge_axes(d.keep_shape, d.keep_stride, d.nkeep, a.keep_shape, a.keep_stride);
+    a.nred = merge_axes(d.red_shape, d.red_stride, d.nred, a.red_shape, a.red_stride);
+    a.nout = 1;
+    a.nterm = 1;
+    for (int i = 0; i < d.nkeep; ++i) a.nout *= d.keep_shape[i];
+    for (int i = 0; i < d.nred; ++i) a.nterm *= d.red_shape[i];
+    const int64_t eb = d.dtype == PE_F16 ? 2 : 4;
+    if (a.nterm == 0) {
+        p.mode = 0;
+        p.V = p.L = 1;
+        a.G = 0;
+        a.C = 1;
+        return p;
+    }
+    if (a.nred == 1 && a.red_stride[0] == 1 && a.nterm >= kRowMinTerms) {
+        p.mode = 1;
+        p.L = 64;
+        bool al = aligned(src, 16);
+        for (int i = 0; i < a.nkeep; ++i) al = al && (a.keep_stride[i] * eb) % 16 == 0;
+        p.V = al ? int(16 / eb) : 1;
+        a.G = ceil_div(a.nterm, int64_t(p.V));
+        while (p.L > 4 && p.L * kLaneGroups > a.G) p.L /= 2;
+        a.L = p.L;
+        const int64_t by_waves = ceil_div(kTargetWaves * (64 / p.L), a.nout);
+        const int64_t by_len = std::max<int64_t>(1, a.G / (int64_t(p.L) * 8));  // each lane at least 8 groups
+        a.C = std::max<int64_t>(1, std::min<int64_t>({by_waves, by_len, kMaxChunks}));
+    } else {
+        p.mode = 2;
+        p.V = p.L = 1;
+        a.G = a.nterm;
+        p.ngroups = ceil_div(a.nout, int64_t(64));
+        const int64_t by_waves = ceil_div(kTargetWaves, p.ngroups);
+        const int64_t by_len = std::max<int64_t>(1, a.nterm / 256);  // each chunk at least 256 terms
+        a.C = std::max<int64_t>(1, std::min<int64_t>({by_waves, by_len, kMaxChunks}));
+    }
+    return p;
+}
+
 }  // namespace
 }  // namespace pe
 
-extern "C" int pe_reduce_axes(const pe_reduce_desc* d, const void* src, float* dst, void* stream) {
+extern "C" int64_t pe_reduce_workspace_bytes(const pe_reduce_desc* d) {
+    using namespace pe;
+    if (!d || validate(*d) != PE_OK) return 0;
+    const RedPlan p = plan_reduce(*d, nullptr);
+    return p.a.C > 1 ? p.a.C * p.a.nout * int64_t(sizeof(float)) : 0;
+}
+
+extern "C" int pe_reduce_order(const pe_reduce_desc* d, const void* src, int64_t* order) {
+    using namespace pe;
+    if (!d || !order) return fail(PE_ERR_INVALID, "reduce_order: null argument");
+    const int st = validate(*d);
+    if (st != PE_OK) return st;
+    const RedPlan p = plan_reduce(*d, src);
+    order[0] = p.V;
+    order[1] = p.L;
+    order[2] = p.a.C;
+    return PE_OK;
+}
+
+extern "C" int pe_reduce_axes(const pe_reduce_desc* d, const void* src, float* dst, void* ws, int64_t ws_bytes,
+                              void* stream) {
     using namespace pe;
     if (!d) return fail(PE_ERR_INVALID, "reduce_axes: null descriptor");
     const int st = validate(*d);
     if (st != PE_OK) return st;
-    ReduceAxesArgs a{};
-    a.src = src;
+    RedPlan p = plan_reduce(*d, src);
+    RedArgs& a = p.a;
     a.dst = dst;
-    a.nkeep = d->nkeep;
-    a.nred = d->nred;
-    a.nout = 1;
-    a.nterm = 1;
-    for (int i = 0; i < d->nkeep; ++i) {
-        a.keep_shape[i] = d->keep_shape[i];
-        a.keep_stride[i] = d->keep_stride[i];
-        a.nout *= d->keep_shape[i];
-    }
-    for (int i = 0; i < d->nred; ++i) {
-        a.red_shape[i] = d->red_shape[i];
-        a.red_stride[i] = d->red_stride[i];
-        a.nterm *= d->red_shape[i];
-    }
     if (a.nout == 0) return PE_OK;
     hipStream_t s = static_cast<hipStream_t>(stream);
+    const int cus = cu_count();
+    if (p.mode == 0) {
+        // No terms: every output is the empty sum, +0 (a kernel, not a
+        // memset, so the call stays capture-safe).
+        const int grid = int(std::max<int64_t>(1, std::min<int64_t>(ceil_div(a.nout, 256), int64_t(cus) * 8)));
+        hipLaunchKernelGGL(zero_kernel, dim3(grid), dim3(256), 0, s, dst, a.nout);
+        PE_CHECK_HIP(hipGetLastError());
+        return PE_OK;
+    }
+    if (a.C > 1) {
+        if (!ws || ws_bytes < a.C * a.nout * int64_t(sizeof(float)))
+            return fail(PE_ERR_WORKSPACE, "reduce_axes: workspace missing or smaller than pe_reduce_workspace_bytes");
+        a.ws = static_cast<float*>(ws);
+    }
     const bool f16 = d->dtype == PE_F16;
-    if (a.nterm > kChunkTerms && a.nout < kWideOutputs) {
-        const int32_t nchunk = int32_t(std::min<int64_t>(kChunkThreads, ceil_div(a.nterm, kChunkTerms)));
-        const int grid = int(std::min<int64_t>(a.nout, int64_t(cu_count()) * 8));
-        if (f16)
-            hipLaunchKernelGGL(reduce_axes_chunked_kernel<F16>, dim3(grid), dim3(kChunkThreads), 0, s, a, nchunk);
-        else
-            hipLaunchKernelGGL(reduce_axes_chunked_kernel<F32>, dim3(grid), dim3(kChunkThreads), 0, s, a, nchunk);
+    if (p.mode == 1) {
+        const int64_t blocks = ceil_div(a.nout * a.C * p.L, int64_t(256));
+        if (blocks >= (int64_t(1) << 31)) return fail(PE_ERR_UNSUPPORTED, "reduce_axes: too many outputs");
+        const dim3 grid{uint32_t(blocks)};
+        if (f16) {
+            if (p.V == 8) hipLaunchKernelGGL((reduce_row_kernel<F16, 8>), grid, dim3(256), 0, s, a);
+            else hipLaunchKernelGGL((reduce_row_kernel<F16, 1>), grid, dim3(256), 0, s, a);
+        } else {
+            if (p.V == 4) hipLaunchKernelGGL((reduce_row_kernel<F32, 4>), grid, dim3(256), 0, s, a);
+            else hipLaunchKernelGGL((reduce_row_kernel<F32, 1>), grid, dim3(256), 0, s, a);
+        }
     } else {
-        const int grid = int(std::max<int64_t>(1, std::min<int64_t>(ceil_div(a.nout, 256), int64_t(cu_count()) * 16)));
-        if (f16)
-            hipLaunchKernelGGL(reduce_axes_kernel<F16>, dim3(grid), dim3(256), 0, s, a);
-        else
-            hipLaunchKernelGGL(reduce_axes_kernel<F32>, dim3(grid), dim3(256), 0, s, a);
+        const int64_t blocks = ceil_div(p.ngroups * a.C, int64_t(4));
+        if (blocks >= (int64_t(1) << 31)) return fail(PE_ERR_UNSUPPORTED, "reduce_axes: too many outputs");
+        const dim3 grid{uint32_t(blocks)};
+        if (f16) hipLaunchKernelGGL(reduce_col_kernel<F16>, grid, dim3(256), 0, s, a, p.ngroups);
+        else hipLaunchKernelGGL(reduce_col_kernel<F32>, grid, dim3(256), 0, s, a, p.ngroups);
     }
     PE_CHECK_HIP(hipGetLastError());
+    if (a.C > 1) {
+        const int grid = int(std::max<int64_t>(1, std::min<int64_t>(a.nout, int64_t(cus) * 8)));
+        hipLaunchKernelGGL(reduce_tree_kernel, dim3(grid), dim3(256), 0, s, a.ws, dst, a.nout, int32_t(a.C));
+        PE_CHECK_HIP(hipGetLastError());
+    }
     return PE_OK;
 }

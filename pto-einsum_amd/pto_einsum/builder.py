@@ -265,9 +265,13 @@ def _reduce_operand(x: torch.Tensor, subs: str, solo: str) -> torch.Tensor:
     d.src_numel = x.untyped_storage().nbytes() // x.element_size() - x.storage_offset()
     out = torch.empty([x.shape[i] for i in keep], dtype=torch.float32, device=x.device)
     lib = abi.bind()
+    ws_bytes = int(lib.pe_reduce_workspace_bytes(ctypes.byref(d)))
+    # Chunk sums of the two-pass order: stream-ordered, freed with the tensor.
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes else None
     with torch.cuda.device(x.device):
         stream = ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream)
-        rc = lib.pe_reduce_axes(ctypes.byref(d), ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(out.data_ptr()), stream)
+        rc = lib.pe_reduce_axes(ctypes.byref(d), ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(out.data_ptr()),
+                                ctypes.c_void_p(ws.data_ptr() if ws is not None else None), ws_bytes, stream)
     runtime.check(rc, "pe_reduce_axes")
     return out
 

@@ -1,11 +1,12 @@
 """Opt-in single-operand reduction axes on the GPU.
 
 The reduction stage (pe_reduce_axes) is checked bit for bit against float32
-loops on the CPU in its documented order: the terms of an output, row-major
-over the reduced index, cut into C contiguous chunks (the first nterm % C one
-term longer), each chunk summed from +0 and the partial sums added in chunk
-order from +0; C = 1 when nterm <= 256 or there are at least 32768 outputs,
-else min(256, ceil(nterm / 256)).  Whole einsums are checked against float64
+loops on the CPU in its documented order, with the (V, L, C) the library
+reports for each call (pe_reduce_order): the terms of an output, row-major
+over the reduced index, form ceil(nterm / V) groups of V; the groups are cut
+into C contiguous chunks (the first G % C one longer); lane l of L sums groups
+l, l + L, ... of its chunk term by term from +0; lane sums, then chunk sums,
+are combined by a pairwise tree.  Whole einsums are checked against float64
 torch.einsum with the contraction tolerance (the reference has no result to
 compare with: it rejects these equations)."""
 import ctypes
@@ -15,69 +16,82 @@ import pytest
 import torch
 
 from pto_einsum import abi, einsum, runtime
+from solo_reduce_order import ordered_sum, reduce_desc
 
 pytestmark = pytest.mark.gpu
 
-CHUNK_TERMS, WIDE_OUTPUTS, CHUNK_THREADS = 256, 32768, 256
+
+def _order(x: torch.Tensor, axes):
+    d = reduce_desc(x, axes)
+    order = (ctypes.c_int64 * 3)()
+    rc = abi.bind().pe_reduce_order(ctypes.byref(d), ctypes.c_void_p(x.data_ptr()), order)
+    runtime.check(rc, "pe_reduce_order")
+    return tuple(int(v) for v in order)
 
 
-def _ordered_sum(x: np.ndarray, axes):
-    """float32 sum over `axes` in the chunked order above, the other axes
-    kept in order.  Each loop step adds one term to every output at once, so
-    the per-output order is sequential."""
-    keep = [i for i in range(x.ndim) if i not in axes]
-    xt = np.transpose(x, keep + list(axes)).astype(np.float32)
-    nout = int(np.prod([x.shape[i] for i in keep], dtype=np.int64))
-    flat = xt.reshape(nout, -1)
-    nterm = flat.shape[1]
-    nchunk = 1 if nterm <= CHUNK_TERMS or nout >= WIDE_OUTPUTS else min(CHUNK_THREADS, -(-nterm // CHUNK_TERMS))
-    q, r = divmod(nterm, nchunk)
-    total = np.zeros(nout, dtype=np.float32)
-    t = 0
-    for c in range(nchunk):
-        acc = np.zeros(nout, dtype=np.float32)
-        for _ in range(q + (1 if c < r else 0)):
-            acc = acc + flat[:, t]
-            t += 1
-        total = total + acc
-    assert t == nterm
-    return total.reshape([x.shape[i] for i in keep])
+def _view(x: torch.Tensor, how: str) -> torch.Tensor:
+    if how == "t":        # a transposed (non-contiguous) view of x's values
+        return x.t().contiguous().cuda().t()
+    if how == "off":      # x's values one element into a larger buffer (rows misaligned)
+        big = torch.zeros(x.shape[0], x.shape[1] + 1, dtype=x.dtype)
+        big[:, 1:] = x
+        return big.cuda()[:, 1:]
+    return x.cuda()
 
 
-def test_ordered_sum_restates_the_plain_loop_for_one_chunk():
-    """The checker itself: with one chunk it is the scalar sequential loop."""
-    x = np.random.default_rng(1).standard_normal((3, 200)).astype(np.float32)
-    want = np.zeros(3, dtype=np.float32)
-    for i in range(3):
-        acc = np.float32(0.0)
-        for v in x[i]:
-            acc = np.float32(acc + v)
-        want[i] = acc
-    assert np.array_equal(_ordered_sum(x, (1,)).view(np.uint32), want.view(np.uint32))
-    # more chunks: the same total to rounding, a different (chunked) order
-    y = np.random.default_rng(2).standard_normal((2, 5000)).astype(np.float32)
-    assert np.allclose(_ordered_sum(y, (1,)), y.astype(np.float64).sum(1), rtol=0, atol=1e-3)
+CASES = [
+    # shape, reduced axes, view, expected mode: "row" (V*L > 1) or "col"
+    ((5, 7, 9), (1,), "", "col"),
+    ((5, 7, 9), (0, 2), "", "col"),              # two reduced runs: odometer
+    ((6, 33), (1,), "t", "col"),
+    ((4, 3), (), "", "col"),                     # conversion only
+    ((3, 0, 2), (1,), "", None),                 # no terms: +0
+    ((3, 70001), (1,), "", "row"),               # few outputs, chunked, partial last group
+    ((2, 37, 300), (1, 2), "", "row"),           # two axes merging into one run
+    ((300, 5), (0,), "t", "row"),
+    ((40000, 300), (1,), "", "row"),
+    ((5000, 300), (1,), "", "row"),              # more than 2048 outputs of more than 256 terms
+    ((64, 1025), (1,), "off", "row"),            # misaligned rows: V = 1
+    ((64, 100000), (1,), "", "row"),             # C > 1 with 64 outputs
+    ((20000, 64), (0,), "", "col"),              # strided reduced axis, C > 1
+    ((300, 8, 200), (0, 2), "", "col"),          # odometer chunks starting mid-run
+    ((7, 20), (1,), "", "col"),                  # short runs go lane-per-output
+    ((1000, 40), (1,), "", "row"),               # four lanes per output, 16 outputs per wave
+]
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16], ids=["f32", "f16"])
-@pytest.mark.parametrize("shape,axes,transpose", [((5, 7, 9), (1,), False), ((5, 7, 9), (0, 2), False),
-                                                  ((6, 33), (1,), True), ((4, 3), (), False),
-                                                  ((3, 0, 2), (1,), False),
-                                                  ((3, 70001), (1,), False), ((2, 37, 300), (1, 2), False),
-                                                  ((300, 5), (0,), True), ((40000, 300), (1,), False)])
-def test_reduce_axes_is_the_sequential_sum(dtype, shape, axes, transpose):
+@pytest.mark.parametrize("shape,axes,how,mode", CASES, ids=[f"{c[0]}-{c[1]}-{c[2]}" for c in CASES])
+def test_reduce_axes_is_the_documented_sum(dtype, shape, axes, how, mode):
     from pto_einsum.builder import _reduce_operand
 
     g = torch.Generator().manual_seed(sum(shape) + len(axes))
     x = torch.randn(*shape, generator=g).to(dtype)
     subs = "abcde"[: len(shape)]
-    xd = x.cuda()
-    if transpose:  # a non-contiguous view
-        xd = x.t().contiguous().cuda().t()
+    xd = _view(x, how)
+    V, L, C = _order(xd, axes)
+    if mode == "row":
+        # groups of 16 bytes when every output's run starts 16-byte aligned
+        eb = x.element_size()
+        keep_strides = [xd.stride(i) for i in range(xd.dim()) if i not in axes and xd.shape[i] > 1]
+        al = xd.data_ptr() % 16 == 0 and all(s * eb % 16 == 0 for s in keep_strides)
+        assert L in (4, 8, 16, 32, 64) and V == (16 // eb if al else 1)
+    elif mode == "col":
+        assert (V, L) == (1, 1)
     got = _reduce_operand(xd, subs, "".join(subs[i] for i in axes)).cpu().numpy()
-    want = _ordered_sum(x.float().numpy(), axes)
+    want = ordered_sum(x.float().numpy(), axes, V, L, C)
     assert got.dtype == np.float32 and got.shape == want.shape
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    again = _reduce_operand(xd, subs, "".join(subs[i] for i in axes)).cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
+
+
+def test_chunked_orders_use_several_chunks():
+    """The cases above reach the two-pass path (C > 1) in both modes."""
+    x = torch.zeros(64, 100000, device="cuda")
+    assert _order(x, (1,))[2] > 1
+    y = torch.zeros(20000, 64, device="cuda")
+    assert _order(y, (0,))[2] > 1
 
 
 EQS = [
@@ -131,11 +145,25 @@ def test_reduce_axes_validation():
     x = torch.zeros(20, device="cuda")
     out = torch.empty(4, device="cuda")
     st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-    rc = lib.pe_reduce_axes(ctypes.byref(d), ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(out.data_ptr()), st)
+    def call(ws=None, ws_bytes=0):
+        return lib.pe_reduce_axes(ctypes.byref(d), ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(out.data_ptr()),
+                                  ctypes.c_void_p(ws), ws_bytes, st)
+
+    rc = call()
     assert rc == -2 and "past the source" in runtime.last_error()
     d.src_numel, d.reserved = 20, 1
-    rc = lib.pe_reduce_axes(ctypes.byref(d), ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(out.data_ptr()), st)
+    rc = call()
     assert rc == -1 and "reserved" in runtime.last_error()
     d.reserved, d.dtype = 0, 7
-    rc = lib.pe_reduce_axes(ctypes.byref(d), ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(out.data_ptr()), st)
+    rc = call()
     assert rc == -3
+    # a chunked order without its workspace: refused before any launch
+    big = torch.zeros(64, 100000, device="cuda")
+    d = reduce_desc(big, (1,))
+    need = int(lib.pe_reduce_workspace_bytes(ctypes.byref(d)))
+    assert need == 64 * _order(big, (1,))[2] * 4
+    out = torch.empty(64, device="cuda")
+    for ws, nb in ((None, 0), (out.data_ptr(), need - 4)):
+        rc = lib.pe_reduce_axes(ctypes.byref(d), ctypes.c_void_p(big.data_ptr()), ctypes.c_void_p(out.data_ptr()),
+                                ctypes.c_void_p(ws), nb, st)
+        assert rc == -4 and "workspace" in runtime.last_error()

@@ -56,3 +56,76 @@ def test_opt_in_needs_gpu_operands():
     a, b = torch.randn(3, 4), torch.randn(4, 5)
     with pytest.raises(ValueError, match="GPU"):
         einsum("ij,jk->k", a, b, device="cpu", reduce_solo_axes=True)
+
+
+# --------------------------------------------- pe_reduce_axes' summation order
+
+from solo_reduce_order import ordered_sum, reduce_desc, scalar_ordered_sum  # noqa: E402
+
+
+@pytest.mark.parametrize("shape,axes,V,L,C", [((3, 1000), (1,), 4, 64, 3), ((2, 37, 30), (1, 2), 8, 64, 1),
+                                              ((5, 7, 9), (0, 2), 1, 1, 4), ((4, 130), (1,), 1, 64, 2),
+                                              ((3, 64), (1,), 4, 64, 5), ((2, 0), (1,), 4, 64, 1)])
+def test_vectorised_order_checker_matches_the_scalar_statement(shape, axes, V, L, C):
+    x = np.random.default_rng(sum(shape)).standard_normal(shape).astype(np.float32) * 1e3
+    x[..., ::7] *= 1e-4  # mixed magnitudes, so that orders differ in the last bits
+    got = ordered_sum(x, axes, V, L, C)
+    want = scalar_ordered_sum(x, axes, V, L, C)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_order_checker_with_one_lane_is_the_sequential_loop():
+    x = np.random.default_rng(1).standard_normal((3, 200)).astype(np.float32)
+    want = np.zeros(3, dtype=np.float32)
+    for i in range(3):
+        acc = np.float32(0.0)
+        for v in x[i]:
+            acc = np.float32(acc + v)
+        want[i] = acc
+    for V in (1, 4):  # groups of consecutive terms do not change a one-lane order
+        assert np.array_equal(ordered_sum(x, (1,), V, 1, 1).view(np.uint32), want.view(np.uint32))
+    # several lanes or chunks: a different order (the same total to rounding)
+    assert not np.array_equal(ordered_sum(x, (1,), 4, 64, 1), want)
+    assert np.allclose(ordered_sum(x, (1,), 4, 64, 3), x.astype(np.float64).sum(1), rtol=0, atol=1e-4)
+
+
+def test_order_checker_sums_exactly_on_integers():
+    x = np.random.default_rng(2).integers(-1000, 1000, size=(6, 5, 777)).astype(np.float32)
+    want = x.astype(np.int64).sum(axis=(0, 2))
+    for V, L, C in ((1, 1, 1), (4, 64, 7), (8, 64, 2), (1, 1, 300)):
+        assert np.array_equal(ordered_sum(x, (0, 2), V, L, C).astype(np.int64), want)
+
+
+def _order_of(x, axes):
+    import ctypes
+
+    from pto_einsum import abi, runtime
+
+    d = reduce_desc(x, axes)
+    out = (ctypes.c_int64 * 3)()
+    runtime.check(abi.bind().pe_reduce_order(ctypes.byref(d), ctypes.c_void_p(x.data_ptr()), out), "order")
+    return tuple(int(v) for v in out), int(abi.bind().pe_reduce_workspace_bytes(ctypes.byref(d)))
+
+
+def test_reduce_order_choice():
+    """Row mode (up to a wave per output, 16-byte groups) when the reduced axes
+    form one contiguous run of >= 32 terms; lane-per-output otherwise; chunks
+    (and a workspace) when outputs are too few to fill the chip."""
+    (o, ws) = _order_of(torch.zeros(5000, 3000), (1,))
+    assert o == (4, 64, 1) and ws == 0
+    (o, ws) = _order_of(torch.zeros(5000, 300), (1,))             # 75 groups: 16 lanes of >= 4
+    assert o == (4, 16, 1) and ws == 0
+    (o, ws) = _order_of(torch.zeros(5000, 304, dtype=torch.float16), (1,))
+    assert o == (8, 8, 1) and ws == 0
+    (o, _) = _order_of(torch.zeros(64, 1026)[:, 1:], (1,))       # rows not 16-byte aligned
+    assert o[:2] == (1, 64)
+    (o, ws) = _order_of(torch.zeros(64, 100000), (1,))
+    assert o[:2] == (4, 64) and o[2] > 1 and ws == 64 * o[2] * 4
+    (o, _) = _order_of(torch.zeros(5000, 100), (1,))             # 25 groups: the fewest lanes
+    assert o == (4, 4, 1)
+    (o, _) = _order_of(torch.zeros(5000, 20), (1,))              # short runs: a lane per output
+    assert o == (1, 1, 1)
+    (o, ws) = _order_of(torch.zeros(20000, 64), (0,))            # strided reduced axis, 64 outputs
+    assert o[:2] == (1, 1) and o[2] > 1 and ws == 64 * o[2] * 4
+    (o, ws) = _order_of(torch.zeros(3, 0, 2), (1,))              # no terms
+    assert ws == 0
