@@ -154,7 +154,7 @@ typedef short i16x4 __attribute__((ext_vector_type(4)));
 // One operand's share of a slab: ROWS rows (m or n) x BK k.  Stateless:
 // per-lane offsets are recomputed from the lane index at each use, so no
 // register stays live across slabs for them.
-template <typename E, int ROWS, int LAYOUT>
+template <typename E, int ROWS, int LAYOUT, bool SMALL_TILE>
 struct DlOperand {
     using T = typename E::T;
     static_assert(LAYOUT == L_MN || LAYOUT == L_K, "direct loads need 16-byte vectors");
@@ -168,10 +168,15 @@ struct DlOperand {
     static constexpr int LPR = ROWS / EPV;            // L_MN: lanes (vectors) per k row
     static constexpr int KPC = 64 / LPR;              // L_MN: k rows per chunk
     static_assert(kF32 || LAYOUT == L_K || LPR >= 8, "float16 k-major swizzle needs 8 vectors per row");
+    // float32 L_K fragments: four k per 16-byte read in tiles of at most
+    // 128 x 128; 256-wide tiles keep 8-byte reads (k pairs), whose smaller
+    // ring fits the register budget of three resident blocks per CU.
+    static constexpr bool kQuadK = kF32 && LAYOUT == L_K && SMALL_TILE;
     // Fragment ring.  float32: L_MN reads one k per step (current + next);
-    // L_K reads k pairs, so two pairs are held.  float16: one 8-element
-    // fragment per step (current + next).
-    static constexpr int RING = !kF32 ? 2 : (LAYOUT == L_MN ? 2 : 4);
+    // L_K reads four k (or a k pair) at a time, the next ones while the
+    // current ones are consumed.  float16: one 8-element fragment per step
+    // (current + next).
+    static constexpr int RING = !kF32 ? 2 : (LAYOUT == L_MN ? 2 : (kQuadK ? 8 : 4));
     using Frag = typename DlMath<E>::Frag;
 
     // float16 k-major swizzle: logical 16-byte group g of k row k sits at
@@ -257,14 +262,27 @@ struct DlOperand {
 
     // Reads what MFMA step st needs for fragment block i (rows 32 i ..
     // 32 i + 31 of the wave, which starts at wrow0) into ring slot
-    // st % RING.  float32 L_K reads k pairs, at even steps only (slots st % 4
-    // and (st + 1) % 4).  All offsets but the lane's are uniform.
+    // st % RING.  float32 L_K reads four k at steps 0 and 4 (slots st ..
+    // st + 3), or k pairs at even steps (slots st % 4 and (st + 1) % 4).
+    // All offsets but the lane's are uniform.
     __device__ __forceinline__ static void frag(const T* stage, const LaneOff& lo, int wrow0, int i, int st,
                                                 Frag (&v)[RING]) {
         if constexpr (kF32 && LAYOUT == L_MN) {
             v[st % 2] = stage[lo.o[0] + st * ROWS + i * 32];
         } else if constexpr (kF32) {
-            if (st % 2 == 0) {
+            // One 16-byte read per lane covers four steps.  A 16-lane phase
+            // of ds_read_b128 spans rows r0 .. r0 + 15, whose (r % 4, group)
+            // pairs are all distinct under the (r / 4) % 4 swizzle: no bank
+            // conflicts.  8-byte reads (k pairs) are processed in 32-lane
+            // phases that pair row r with row r + 16 on the same banks: two
+            // ways in conflict.
+            if constexpr (kQuadK) {
+                if (st % 4 == 0) {
+                    const f32x4 x = *reinterpret_cast<const f32x4*>(stage + lo.o[st / 4] + i * 32 * BK);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[st + e] = x[e];
+                }
+            } else if (st % 2 == 0) {
                 typedef float f32x2 __attribute__((ext_vector_type(2)));
                 const f32x2 x = *reinterpret_cast<const f32x2*>(stage + lo.o[st / 4] + i * 32 * BK + st % 4);
                 v[st % 4] = x[0];
@@ -292,8 +310,8 @@ template <typename E, int BM, int BN, int AL, int BL, int MINB>
 __global__ __launch_bounds__(kGemmThreads, MINB) void gemm_dl_kernel(GemmArgs g) {
     using T = typename E::T;
     using M = DlMath<E>;
-    using OA = DlOperand<E, BM, AL>;
-    using OB = DlOperand<E, BN, BL>;
+    using OA = DlOperand<E, BM, AL, (BM <= 128 && BN <= 128)>;
+    using OB = DlOperand<E, BN, BL, (BM <= 128 && BN <= 128)>;
     constexpr int BK = M::BK;
     constexpr int WM = BM / 2, WN = BN / 2;
     constexpr int FM = WM / 32, FN = WN / 32;
