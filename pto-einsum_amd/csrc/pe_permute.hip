@@ -27,14 +27,18 @@ namespace {
 
 constexpr int kThreads = 256;
 
-// Gather stream shape for outputs the Infinity Cache holds (measured on
-// MI355X: many resident waves, two 16-byte vectors in flight per lane);
-// larger outputs take a flat launch with non-temporal stores (see run()).
+// Gather stream shape of the persistent grid (many resident waves, two
+// 16-byte vectors in flight per lane), used for unaligned gathers; aligned
+// ones take a flat launch, one vector per thread (PE_GATHER_FLAT, see run()),
+// with non-temporal stores for outputs beyond the Infinity Cache.
 #ifndef PE_GATHER_GRID_PER_CU
 #define PE_GATHER_GRID_PER_CU 64
 #endif
 #ifndef PE_GATHER_UNROLL
 #define PE_GATHER_UNROLL 2
+#endif
+#ifndef PE_GATHER_FLAT
+#define PE_GATHER_FLAT 1
 #endif
 
 struct GatherArgs {
@@ -277,14 +281,13 @@ int run(const pe_permute_desc& d, const void* src, void* dst, hipStream_t s) {
         for (int k = 0; k < a.nouter && vec; ++k) vec = sst[k] % VEC == 0;
         const bool outer = a.nouter > 0;
         const int per_cu = PE_GATHER_GRID_PER_CU;
-        if (vec && a.nt) {
-            // Outputs beyond the Infinity Cache: one vector per thread in a
-            // grid of blocks dispatched in address order, so the blocks in
-            // flight read and write one compact window of HBM.  Measured on
-            // MI355X: 1 GiB copy 4.99 -> 6.37 TB/s, config 3's output
-            // permutation (2.15 GB) 923 -> 714 us, against the persistent
-            // grid-stride stream below, whose drifting blocks scatter their
-            // writes over many DRAM pages.
+        if (vec && (a.nt || PE_GATHER_FLAT)) {
+            // One vector per thread in a grid of blocks dispatched in address
+            // order, so the blocks in flight read and write one compact
+            // window of HBM.  Measured on MI355X: 1 GiB copy 4.99 -> 6.37
+            // TB/s, config 3's output permutation (2.15 GB) 923 -> 714 us,
+            // against the persistent grid-stride stream below, whose
+            // drifting blocks scatter their writes over many DRAM pages.
             a.nvec = uint32_t(n / VEC);
             a.inner_vecs.init(uint32_t(inner / VEC));
             const int grid = int(ceil_div(a.nvec, kThreads));
