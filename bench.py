@@ -385,13 +385,13 @@ def chain_case(precise):
     (pto_einsum.linear_attention): q, k float16 normal(0, 1/sqrt(128)), v
     float16 normal(0, 1), the causal decay mask gamma^(t-s), gamma = 0.995,
     in float32; t = s = 4096, n = p = 128.  The default launch computes P.V
-    as three bfloat16 MFMA terms of the split P and V; ``precise`` puts P.V on
-    float32 MFMAs.  The roof is the larger of the compulsory HBM bytes (q, k,
-    v, m read once, out written once) at 8 TB/s and the MFMAs the launch
-    issues for the dense chain (2*T*S*N float16 flops plus, for the default,
-    3 * 2*T*S*P bfloat16 flops at the 16-bit peak, for precise 2*T*S*P at
-    the float32 peak); zero mask blocks are skipped, so the causal case does
-    less."""
+    at float32 accuracy on bfloat16 MFMAs (P in three terms, the float16 V in
+    two: five products per k step); ``precise`` puts P.V on float32 MFMAs.
+    The roof is the larger of the compulsory HBM bytes (q, k, v, m read once,
+    out written once) at 8 TB/s and the MFMAs the launch issues for the dense
+    chain (2*T*S*N float16 flops plus, for the default, 5 * 2*T*S*P bfloat16
+    flops at the 16-bit peak, for precise 2*T*S*P at the float32 peak); zero
+    mask blocks are skipped, so the causal case does less."""
     import torch
 
     from pto_einsum import linear_attention
@@ -419,10 +419,10 @@ def chain_case(precise):
         if precise:
             mfma_ms = (2 * T * S * N / PEAK_TFLOPS["f16"] + 2 * T * S * P / PEAK_TFLOPS["f32"]) / 1e12 * 1e3
         else:
-            mfma_ms = (2 * T * S * N + 3 * 2 * T * S * P) / (PEAK_TFLOPS["f16"] * 1e12) * 1e3
+            mfma_ms = (2 * T * S * N + 5 * 2 * T * S * P) / (PEAK_TFLOPS["f16"] * 1e12) * 1e3
         floor_ms = max(hbm_ms, mfma_ms)
         row = dict(config="5.F" + (" precise" if precise else ""), equation="tn,sn,sp,ts->tp (fused)",
-                   dtype="f16 q/k, f32 chain, P.V " + ("f32 MFMA" if precise else "3 bf16 terms"),
+                   dtype="f16 q/k, f32 chain, P.V " + ("f32 MFMA" if precise else "f32-accurate bf16x3"),
                    us=round(ms * 1e3, 2), tflops=round(flops / (ms * 1e-3) / 1e12, 3),
                    gbs=round(nbytes / (ms * 1e-3) / 1e9, 1), roof="hbm" if hbm_ms >= mfma_ms else "mfma",
                    frac=round(floor_ms / ms, 4), floor_us=round(floor_ms * 1e3, 2), sets=nsets)

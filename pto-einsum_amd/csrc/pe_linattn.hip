@@ -16,17 +16,22 @@
 //      s = 8*(r/4) + 4*(l/32) + r%4, r = 0..15.
 //   2. Those 16 values are multiplied by the mask in registers (one float32
 //      rounding, as the Hadamard step).
-//   3. P.V, by default on bfloat16 matrix cores: the 16 values are split into
-//      bfloat16 hi + lo (round to nearest even; x - hi is exact) and become
-//      the A operands of two v_mfma_f32_32x32x16_bf16 k-steps whose k order
-//      is permuted to match (step q2, lane half h, slot j <-> s = 16*q2 +
-//      8*(j/4) + 4*h + j%4).  V is split the same way when it is staged,
-//      transposed and in that permuted order, so one 16-byte LDS read gives a
-//      lane its eight k slots.  P.V = Phi.Vhi + Phi.Vlo + Plo.Vhi: products
-//      exact, sums float32, each dropped part below 2^-16 |P||V| (a float16 V
-//      splits exactly).  With `precise` the 16 values instead feed sixteen
-//      float32 MFMAs (v_mfma_f32_32x32x2_f32), MFMA j pairing lane half h with
-//      s = 8*(j/4) + 4*h + j%4, from a float32 transposed V tile.
+//   3. P.V, by default on bfloat16 matrix cores at float32 accuracy: the 16
+//      values are split into three bfloat16 terms P0 + P1 + P2 (round to
+//      nearest even, each term taking 8 more significant bits, remainders
+//      exact; what is left is below 2^-24 |P|) and become the A operands of
+//      v_mfma_f32_32x32x16_bf16 k-steps whose k order is permuted to match
+//      (step q2, lane half h, slot j <-> s = 16*q2 + 8*(j/4) + 4*h + j%4).
+//      V is split the same way when it is staged (two terms, exact, for a
+//      float16 V; three for a float32 one), transposed and in that permuted
+//      order, so one 16-byte LDS read gives a lane its eight k slots.
+//      P.V = sum of Pi.Vj over i + j <= 2: five MFMAs (float16 V) or six,
+//      products exact, sums float32; everything left out is below
+//      2^-22 |P||V| per product -- the bfloat16x3 technique of emulating
+//      float32 products on 16-bit matrix cores.  With `precise` the 16 values
+//      instead feed sixteen float32 MFMAs (v_mfma_f32_32x32x2_f32), MFMA j
+//      pairing lane half h with s = 8*(j/4) + 4*h + j%4, from a float32
+//      transposed V tile.
 //
 // Blocks of 32 t x 32 s whose mask is zero everywhere are skipped: their
 // contribution is exactly +-0 for finite operands.  The s axis is split over
@@ -48,38 +53,56 @@
 namespace pe {
 namespace {
 
-constexpr int kTB = 128;       // t rows per block (four waves x 32)
+// t rows per block: 32 per wave, four or eight waves (PE_LINATTN_WAVES).
+// Eight waves share each staged K / V tile among 256 t rows, which halves
+// the K / V traffic through L2 against four.
+#ifndef PE_LINATTN_WAVES
+#define PE_LINATTN_WAVES 8
+#endif
+constexpr int kWaves = PE_LINATTN_WAVES;
+static_assert(kWaves == 4 || kWaves == 8, "four or eight waves per block");
+constexpr int kThreadsLA = 64 * kWaves;
+constexpr int kTB = 32 * kWaves;
 constexpr int kPB = 128;       // p columns per block (four 32-column MFMA blocks)
 constexpr int kSB = 32;        // s per step
 constexpr int kVLD = kSB + 4;  // LDS pitch of the transposed float32 V tile (conflict-free 16-byte reads)
 constexpr int kVBLD = kSB + 8; // LDS pitch (bf16) of the split V tile: 80-byte rows, conflict-free 16-byte reads
 
 // V tile of one s step, transposed ([p][s]).  Float32 P.V: the float32
-// values.  Split P.V: V = hi + lo as two bfloat16 arrays whose s order is
-// permuted so that one 16-byte read gives a lane its eight k slots of a
-// 32x32x16 MFMA (see the P.V step).
+// values.  Split P.V: V = t[0] + t[1] (+ t[2]) as NV bfloat16 arrays (two
+// terms hold a float16 value exactly, three a float32 one to 2^-24) whose s
+// order is permuted so that one 16-byte read gives a lane its eight k slots
+// of a 32x32x16 MFMA (see the P.V step).
 struct VTileF32 {
     float v[kPB][kVLD];
 };
+template <int NV>
 struct VTileSplit {
-    uint16_t hi[kPB][kVBLD];
-    uint16_t lo[kPB][kVBLD];
+    uint16_t t[NV][kPB][kVBLD];
 };
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-// Round-to-nearest-even split of two float32 into bfloat16 terms: x = hi +
-// lo + e with |e| <= 2^-16 |x| (hi carries the top 8 significant bits, lo the
-// next 8; x - hi is exact in float32).  hi and lo come back packed, x0's term
-// in the low half: each pair conversion is one v_cvt_pk_bf16_f32.
+// Round-to-nearest-even split of two float32 into NT bfloat16 terms:
+// x = t[0] + ... + t[NT-1] + e.  Each term is the bfloat16 nearest to what
+// the previous ones left (an 8-bit significand: |remainder| <= 2^-8 |what was
+// split|), and every remainder is exact in float32, so |e| <= 2^-(8 NT) |x|:
+// 2^-24 |x| for three terms, as fine as float32 itself.  Terms come back
+// packed, x0's in the low half: each pair conversion is one
+// v_cvt_pk_bf16_f32.
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ void split_bf16x2(float x0, float x1, uint32_t& hi, uint32_t& lo) {
-    const f32x2_t x = {x0, x1};
-    hi = __builtin_bit_cast(uint32_t, __builtin_convertvector(x, bf16x2_t));
-    const float h0 = __builtin_bit_cast(float, hi << 16), h1 = __builtin_bit_cast(float, hi & 0xffff0000u);
-    const f32x2_t r = {x0 - h0, x1 - h1};
-    lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(r, bf16x2_t));
+template <int NT>
+__device__ __forceinline__ void split_bf16x2(float x0, float x1, uint32_t (&t)[NT]) {
+    f32x2_t x = {x0, x1};
+#pragma unroll
+    for (int i = 0; i < NT; ++i) {
+        t[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(x, bf16x2_t));
+        if (i + 1 < NT) {
+            const f32x2_t h = {__builtin_bit_cast(float, t[i] << 16), __builtin_bit_cast(float, t[i] & 0xffff0000u)};
+            x = x - h;
+        }
+    }
 }
 
 struct LinAttnArgs {
@@ -131,20 +154,20 @@ struct KTile {
     static constexpr int PITCH = COLS + (QK::kBytes == 2 ? 8 : 4);
     static constexpr int VEC = 16 / QK::kBytes;
     static constexpr int CPR = COLS / VEC;                 // chunks per row
-    static constexpr int PER_THREAD = kSB * CPR / 256;
-    static_assert(kSB * CPR % 256 == 0, "chunks split evenly over the block");
+    static constexpr int PER_THREAD = kSB * CPR / kThreadsLA;
+    static_assert(kSB * CPR % kThreadsLA == 0, "chunks split evenly over the block");
 };
 
 // NSTEPS: MFMA k steps covering N (N <= NSTEPS * KSTEP); VE / ME: element
-// types of v and m; PV32: P.V on float32 MFMAs (else on three bfloat16 MFMA
-// terms, hi*hi + hi*lo + lo*hi of the split P and V).
+// types of v and m; PV32: P.V on float32 MFMAs (else on five or six bfloat16
+// MFMAs over the three-term split of P and the two- or three-term split of V).
 //
 // Per s step (32 s), software-pipelined one step ahead: the V tile (32 x 128,
 // staged transposed), the K tile and this lane's mask values of step i+1 are
 // loaded into registers (raw element type, converted when committed) while
 // step i computes from LDS; two LDS stages mean one barrier per step.
 template <typename QK, int NSTEPS, typename VE, typename ME, bool PV32>
-__global__ __launch_bounds__(256, 2) void linattn_kernel(LinAttnArgs a) {
+__global__ __launch_bounds__(kThreadsLA, 8 / kWaves) void linattn_kernel(LinAttnArgs a) {
     using T = typename QK::T;
     using VT = typename VE::T;
     using MT = typename ME::T;
@@ -152,7 +175,9 @@ __global__ __launch_bounds__(256, 2) void linattn_kernel(LinAttnArgs a) {
     using KT = KTile<QK, NSTEPS>;
     using KChunk = typename Pack<KT::VEC, T>::type;
     using MV = typename Pack<4, MT>::type;
-    using VTile = std::conditional_t<PV32, VTileF32, VTileSplit>;
+    // bfloat16 terms of V: a float16 value splits exactly into two.
+    constexpr int NV = VE::kBytes == 2 ? 2 : 3;
+    using VTile = std::conditional_t<PV32, VTileF32, VTileSplit<NV>>;
     __shared__ __attribute__((aligned(16))) VTile vt[2];                     // V tile, transposed: [p][s]
     __shared__ __attribute__((aligned(16))) T kt[2][kSB * KT::PITCH];       // K tile: [s][n]
 
@@ -183,16 +208,22 @@ __global__ __launch_bounds__(256, 2) void linattn_kernel(LinAttnArgs a) {
         for (int r = 0; r < 16; ++r) acc[j][r] = 0.0f;
 
     // Registers of the step in flight, and this thread's fixed load addresses.
-    const int vp = tid & 127, vs0 = (tid >> 7) * 16;  // this thread's V column and 16 s rows
-    VT vpre[16];
-    KChunk kpre[KT::PER_THREAD];
-    MV mpre[4];
+    // This thread's V column and VROWS consecutive s rows of each step.
+    constexpr int VROWS = kSB * kPB / kThreadsLA;
+    static_assert(VROWS == 8 || VROWS == 16, "V rows per thread");
+    const int vp = tid & 127, vs0 = (tid >> 7) * VROWS;
+    // Registers of the step in flight.
+    struct Pre {
+        VT v[VROWS];
+        KChunk k[KT::PER_THREAD];
+        MV m[4];
+    };
     const VT* vrow0 = static_cast<const VT*>(a.v) + int64_t(vs0) * a.v_ss + min(p0 + vp, a.P - 1);
     const T* krow0[KT::PER_THREAD];
     bool kcol_ok[KT::PER_THREAD];
 #pragma unroll
     for (int i = 0; i < KT::PER_THREAD; ++i) {
-        const int c = tid + 256 * i, col = (c % KT::CPR) * KT::VEC;
+        const int c = tid + kThreadsLA * i, col = (c % KT::CPR) * KT::VEC;
         kcol_ok[i] = col < a.NP;
         krow0[i] = static_cast<const T*>(a.k) + int64_t(c / KT::CPR) * a.k_ss + (kcol_ok[i] ? col : 0);
     }
@@ -203,102 +234,114 @@ __global__ __launch_bounds__(256, 2) void linattn_kernel(LinAttnArgs a) {
     // step later, so nothing waits on the loads here.  A step whose 32 s all
     // lie inside S needs no clamping (the usual case); V columns past P feed
     // only outputs that are never stored, so they are not masked at all.
-    auto prefetch = [&](int sb) {
+    auto prefetch = [&](Pre& P, int sb) {
         if (sb + kSB <= a.S) {
             const VT* vp_ = vrow0 + int64_t(sb) * a.v_ss;
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                vpre[i] = *vp_;
+            for (int i = 0; i < VROWS; ++i) {
+                P.v[i] = *vp_;
                 vp_ += a.v_ss;
             }
 #pragma unroll
             for (int i = 0; i < KT::PER_THREAD; ++i)
-                kpre[i] = *reinterpret_cast<const KChunk*>(krow0[i] + int64_t(sb) * a.k_ss);
+                P.k[i] = *reinterpret_cast<const KChunk*>(krow0[i] + int64_t(sb) * a.k_ss);
 #pragma unroll
-            for (int q = 0; q < 4; ++q) mpre[q] = *reinterpret_cast<const MV*>(mrow4 + sb + 8 * q);
+            for (int q = 0; q < 4; ++q) P.m[q] = *reinterpret_cast<const MV*>(mrow4 + sb + 8 * q);
         } else {
 #pragma unroll
-            for (int i = 0; i < 16; ++i)
-                vpre[i] = vrow0[int64_t(min(sb + vs0 + i, a.S - 1) - vs0) * a.v_ss];
+            for (int i = 0; i < VROWS; ++i)
+                P.v[i] = vrow0[int64_t(min(sb + vs0 + i, a.S - 1) - vs0) * a.v_ss];
 #pragma unroll
             for (int i = 0; i < KT::PER_THREAD; ++i) {
-                const int s = sb + (tid + 256 * i) / KT::CPR;
-                kpre[i] = *reinterpret_cast<const KChunk*>(krow0[i] +
+                const int s = sb + (tid + kThreadsLA * i) / KT::CPR;
+                P.k[i] = *reinterpret_cast<const KChunk*>(krow0[i] +
                                                            int64_t(min(s, a.S - 1) - (s - sb)) * a.k_ss);
             }
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int s = sb + 8 * q + 4 * h;
-                mpre[q] = *reinterpret_cast<const MV*>(mrow4 - 4 * h + (s < a.SP ? s : 0));
+                P.m[q] = *reinterpret_cast<const MV*>(mrow4 - 4 * h + (s < a.SP ? s : 0));
             }
         }
     };
 
-    // Writes this thread's 16 V values (s = vs0 .. vs0+15 of column vp) into
-    // a stage: float32, or split into bf16 hi / lo at the permuted positions
-    // 8*h + j <-> s = 8*(j/4) + 4*h + j%4 of the 16-s group.
+    // Writes this thread's VROWS V values (s = vs0 .. vs0+VROWS-1 of column
+    // vp) into a stage: float32, or split into bf16 hi / lo at the permuted
+    // positions 8*hh + j <-> s = 8*(j/4) + 4*hh + j%4 of each 16-s group.
     auto commit_v = [&](int st, auto val) {
         if constexpr (PV32) {
 #pragma unroll
-            for (int i = 0; i < 16; i += 4) {
+            for (int i = 0; i < VROWS; i += 4) {
                 f32x4 w = {val(i), val(i + 1), val(i + 2), val(i + 3)};
                 *reinterpret_cast<f32x4*>(&vt[st].v[vp][vs0 + i]) = w;
             }
-        } else {
+        } else if constexpr (VROWS == 16) {
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh) {
-                u32x4 wh, wl;
-                uint32_t h4[4], l4[4];
+                uint32_t w[4][NV];
 #pragma unroll
                 for (int j = 0; j < 8; j += 2)
-                    split_bf16x2(val(8 * (j / 4) + 4 * hh + j % 4), val(8 * ((j + 1) / 4) + 4 * hh + (j + 1) % 4),
-                                 h4[j / 2], l4[j / 2]);
-                wh = u32x4{h4[0], h4[1], h4[2], h4[3]};
-                wl = u32x4{l4[0], l4[1], l4[2], l4[3]};
-                *reinterpret_cast<u32x4*>(&vt[st].hi[vp][vs0 + 8 * hh]) = wh;
-                *reinterpret_cast<u32x4*>(&vt[st].lo[vp][vs0 + 8 * hh]) = wl;
+                    split_bf16x2<NV>(val(8 * (j / 4) + 4 * hh + j % 4), val(8 * ((j + 1) / 4) + 4 * hh + (j + 1) % 4),
+                                     w[j / 2]);
+#pragma unroll
+                for (int e = 0; e < NV; ++e)
+                    *reinterpret_cast<u32x4*>(&vt[st].t[e][vp][vs0 + 8 * hh]) = u32x4{w[0][e], w[1][e], w[2][e], w[3][e]};
+            }
+        } else {
+            // Half a 16-s group (a = 0: s 0..7 of the group, a = 1: s 8..15):
+            // s = 8a + 4hh + i (i < 4) sits at position 8hh + 4a + i.
+            typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+            const int g16 = vs0 & ~15, a8 = (vs0 & 15) >> 3;
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                uint32_t w[2][NV];
+#pragma unroll
+                for (int i = 0; i < 4; i += 2) split_bf16x2<NV>(val(4 * hh + i), val(4 * hh + i + 1), w[i / 2]);
+#pragma unroll
+                for (int e = 0; e < NV; ++e)
+                    *reinterpret_cast<u32x2*>(&vt[st].t[e][vp][g16 + 8 * hh + 4 * a8]) = u32x2{w[0][e], w[1][e]};
             }
         }
     };
 
-    if (s_begin < s_end) prefetch(s_begin);
-    int stage = 0;
-    for (int sb = s_begin; sb < s_end; sb += kSB, stage ^= 1) {
+    // One step from registers P (loaded one step earlier) into LDS stage
+    // `stage`, then its MFMAs; P is refilled with step sb + kSB.
+    auto step = [&](Pre& P, const int sb, const int stage) {
         // Commit the prefetched step to this stage (its readers from two steps
         // ago passed the previous barrier after finishing), zeroing what lies
         // past S or N.
         const bool full = sb + kSB <= a.S;
         float mv[16];
         if (full) {
-            commit_v(stage, [&](int i) { return float(vpre[i]); });
+            commit_v(stage, [&](int i) { return float(P.v[i]); });
 #pragma unroll
             for (int i = 0; i < KT::PER_THREAD; ++i) {
-                const int c = tid + 256 * i;
+                const int c = tid + kThreadsLA * i;
                 *reinterpret_cast<KChunk*>(&kt[stage][(c / KT::CPR) * KT::PITCH + (c % KT::CPR) * KT::VEC]) =
-                    k_all_cols ? kpre[i] : zero_unless(kcol_ok[i], kpre[i]);
+                    k_all_cols ? P.k[i] : zero_unless(kcol_ok[i], P.k[i]);
             }
 #pragma unroll
             for (int q = 0; q < 4; ++q)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) mv[4 * q + i] = float(mpre[q][i]);
+                for (int i = 0; i < 4; ++i) mv[4 * q + i] = float(P.m[q][i]);
         } else {
-            commit_v(stage, [&](int i) { return sb + vs0 + i < a.S ? float(vpre[i]) : 0.0f; });
+            commit_v(stage, [&](int i) { return sb + vs0 + i < a.S ? float(P.v[i]) : 0.0f; });
 #pragma unroll
             for (int i = 0; i < KT::PER_THREAD; ++i) {
-                const int c = tid + 256 * i;
+                const int c = tid + kThreadsLA * i;
                 const bool ok = sb + c / KT::CPR < a.S && kcol_ok[i];
                 *reinterpret_cast<KChunk*>(&kt[stage][(c / KT::CPR) * KT::PITCH + (c % KT::CPR) * KT::VEC]) =
-                    zero_unless(ok, kpre[i]);
+                    zero_unless(ok, P.k[i]);
             }
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const bool ok = sb + 8 * q + 4 * h < a.SP;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) mv[4 * q + i] = ok ? float(mpre[q][i]) : 0.0f;
+                for (int i = 0; i < 4; ++i) mv[4 * q + i] = ok ? float(P.m[q][i]) : 0.0f;
             }
         }
         __syncthreads();
-        if (sb + kSB < s_end) prefetch(sb + kSB);
+        if (sb + kSB < s_end) prefetch(P, sb + kSB);
 
         // Any mask value other than +-0 (or of the bits, sign dropped).
         uint32_t mbits = 0;
@@ -344,28 +387,42 @@ __global__ __launch_bounds__(256, 2) void linattn_kernel(LinAttnArgs a) {
                 // bf16 32x32x16 MFMA step q2 covers s = 16*q2 .. 16*q2+15:
                 // lane half h, k slot j holds register r = 8*q2 + j, i.e.
                 // s = 16*q2 + 8*(j/4) + 4*h + j%4, matching the V positions.
-                // P.V = Phi.Vhi + Phi.Vlo + Plo.Vhi (products exact, float32
-                // sums; the dropped Plo.Vlo and the split remainders are each
-                // below 2^-16 |P||V|).
+                // P = P0 + P1 + P2 and V = V0 + V1 (+ V2) in bfloat16 terms;
+                // P.V = sum of Pi.Vj over i + j <= 2 (products exact, float32
+                // sums).  Left out: the split remainders (<= 2^-24 |P| and
+                // |V|) and the terms with i + j > 2 (each <= 2^-24 |P||V|,
+                // one for a float16 V, three for a float32 one): at most
+                // 2^-22 |P||V| per product, float32's own rounding scale.
 #pragma unroll
                 for (int q2 = 0; q2 < 2; ++q2) {
-                    uint32_t h4[4], l4[4];
+                    uint32_t w[4][3];
 #pragma unroll
-                    for (int j = 0; j < 8; j += 2) split_bf16x2(av[8 * q2 + j], av[8 * q2 + j + 1], h4[j / 2], l4[j / 2]);
-                    const u32x4 phw = {h4[0], h4[1], h4[2], h4[3]}, plw = {l4[0], l4[1], l4[2], l4[3]};
-                    const bf16x8 ph = __builtin_bit_cast(bf16x8, phw), pl = __builtin_bit_cast(bf16x8, plw);
+                    for (int j = 0; j < 8; j += 2) split_bf16x2<3>(av[8 * q2 + j], av[8 * q2 + j + 1], w[j / 2]);
+                    bf16x8 pt[3];
+#pragma unroll
+                    for (int e = 0; e < 3; ++e) pt[e] = __builtin_bit_cast(bf16x8, u32x4{w[0][e], w[1][e], w[2][e], w[3][e]});
 #pragma unroll
                     for (int jb = 0; jb < 4; ++jb) {
-                        const bf16x8 vh = *reinterpret_cast<const bf16x8*>(&vt[stage].hi[32 * jb + l32][16 * q2 + 8 * h]);
-                        const bf16x8 vl = *reinterpret_cast<const bf16x8*>(&vt[stage].lo[32 * jb + l32][16 * q2 + 8 * h]);
-                        acc[jb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ph, vh, acc[jb], 0, 0, 0);
-                        acc[jb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ph, vl, acc[jb], 0, 0, 0);
-                        acc[jb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pl, vh, acc[jb], 0, 0, 0);
+                        bf16x8 vv[NV];
+#pragma unroll
+                        for (int e = 0; e < NV; ++e)
+                            vv[e] = *reinterpret_cast<const bf16x8*>(&vt[stage].t[e][32 * jb + l32][16 * q2 + 8 * h]);
+#pragma unroll
+                        for (int i = 0; i < 3; ++i)
+#pragma unroll
+                            for (int j = 0; j < NV; ++j)
+                                if (i + j <= 2) acc[jb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pt[i], vv[j], acc[jb], 0, 0, 0);
                     }
                 }
             }
         }
-    }
+    };
+
+    // (A deeper register prefetch, two steps ahead, measured no faster on
+    // config 5 and spilled in the float32-q/k instantiations.)
+    Pre pre;
+    if (s_begin < s_end) prefetch(pre, s_begin);
+    for (int sb = s_begin, stage = 0; sb < s_end; sb += kSB, stage ^= 1) step(pre, sb, stage);
 
     // Store: lane l, register r holds out[t0 + 8*(r/4) + 4*h + r%4][p0 + 32*jb + l32].
     float* out = a.out + int64_t(blockIdx.z) * a.T * a.P;
@@ -409,7 +466,8 @@ Plan plan(const pe_linattn_desc& d, const void* q, const void* k, const void* m)
     Plan p{};
     const int64_t blocks_tp = ceil_div(d.T, kTB) * ceil_div(d.P, kPB);
     const int64_t sblocks = std::max<int64_t>(1, ceil_div(d.S, kSB));
-    int64_t split = d.split > 0 ? d.split : ceil_div(2 * int64_t(cu_count()), blocks_tp);
+    // About eight waves per CU: two blocks of four or one of eight.
+    int64_t split = d.split > 0 ? d.split : ceil_div(int64_t(cu_count()) * (8 / kWaves), blocks_tp);
     split = std::max<int64_t>(1, std::min(split, sblocks));
     p.s_per_split = int(ceil_div(sblocks, split) * kSB);
     p.nsplit = int(ceil_div(std::max<int64_t>(d.S, 1), p.s_per_split));
@@ -456,9 +514,9 @@ int validate(const pe_linattn_desc& d) {
 template <typename QK, int NSTEPS, typename VE, typename ME>
 hipError_t launch(const LinAttnArgs& a, bool pv32, dim3 grid, hipStream_t s) {
     if (pv32)
-        hipLaunchKernelGGL((linattn_kernel<QK, NSTEPS, VE, ME, true>), grid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL((linattn_kernel<QK, NSTEPS, VE, ME, true>), grid, dim3(kThreadsLA), 0, s, a);
     else
-        hipLaunchKernelGGL((linattn_kernel<QK, NSTEPS, VE, ME, false>), grid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL((linattn_kernel<QK, NSTEPS, VE, ME, false>), grid, dim3(kThreadsLA), 0, s, a);
     return hipGetLastError();
 }
 

@@ -19,11 +19,14 @@ float32); sums are taken in a different order, so agreement is to contraction
 tolerance, not bit for bit.
 
 The last product P.V (P = the masked scores) runs by default on bfloat16
-matrix cores: P and V are each split into bfloat16 hi + lo (round to nearest
-even; x - hi is exact) and P.V = Phi.Vhi + Phi.Vlo + Plo.Vhi with exact
-products and float32 sums.  Each term left out (Plo.Vlo, the split remainders)
-is below 2^-16 |P||V|; a float16 V splits exactly.  ``precise=True`` runs P.V
-on float32 matrix cores instead (eight times the MFMA time of that product).
+matrix cores at float32 accuracy: P is split into three bfloat16 terms and V
+into two (float16, exact) or three (float32), each term the bfloat16 nearest
+to what the previous ones left (round to nearest even; the remainders are
+exact in float32), and P.V is the sum of the term products Pi.Vj with
+i + j <= 2 -- products exact, sums float32.  What is left out is below
+2^-22 |P||V| per product, the scale of float32's own rounding.
+``precise=True`` runs P.V on float32 matrix cores instead (about three times
+the MFMA time of that product).
 """
 from __future__ import annotations
 

@@ -69,10 +69,12 @@ def test_shapes_and_dtypes(T, S, N, P, qk, vd, md, dense, precise):
 
 @pytest.mark.parametrize("vd", [torch.float16, torch.float32], ids=["v16", "v32"])
 def test_split_pv_error_bound(vd):
-    """The default P.V (bfloat16 hi/lo terms) against float32 MFMAs on the
-    same inputs, and both against a float64 evaluation: the split's error is
-    bounded by about 2^-15 sum_s |P||V| per output (three dropped terms below
-    2^-16 |P||V| each plus float32 rounding)."""
+    """The default P.V (bfloat16 terms at float32 accuracy) against float32
+    MFMAs on the same inputs, and both against a float64 evaluation: the
+    split leaves out at most 2^-22 |P||V| per product, so its error is that
+    of float32 arithmetic -- bounded here by 2^-20 sum_s |P||V| per output
+    (float32 accumulation over 2048 terms included), with a mean no larger
+    than 1.25 times the float32 MFMAs' own."""
     g = torch.Generator().manual_seed(50)
     T, S, N, P = 512, 2048, 128, 128
     q = (torch.randn(T, N, generator=g) * N ** -0.5).half()
@@ -84,10 +86,11 @@ def test_split_pv_error_bound(vd):
     qc, kc, vc, mc = (x.cuda().double() for x in (q, k, v, m))
     pm = (qc @ kc.T.contiguous()) * mc
     ref = pm @ vc
-    bound = (pm.abs() @ vc.abs()) * 2.0 ** -15
+    bound = (pm.abs() @ vc.abs()) * 2.0 ** -20
     err_split = (split.cuda().double() - ref).abs()
     err_f32 = (f32.cuda().double() - ref).abs()
     assert bool((err_split <= bound + 1e-30).all()), float((err_split / bound).max())
+    assert float(err_split.mean()) <= 1.25 * float(err_f32.mean())
     assert float(err_split.max()) <= 1e-5 * float(ref.abs().max())
     assert float(err_f32.max()) <= 1e-5 * float(ref.abs().max())
 
