@@ -445,6 +445,51 @@ def large_f16_cases():
             for eq, lab in (("ij,jk->ik", "NN"), ("ik,jk->ij", "NT"))]
 
 
+# Opt-in solo-axis reduction (pe_reduce_axes): (label, shape, reduced axes, dtype); the
+# operands are 0.5-1 GiB, so every call reads cold data.
+SOLO_REDUCE = (
+    ("f32 [64,4000000] sum(1)", (64, 4_000_000), (1,), "f32"),
+    ("f32 [1024,250000] sum(1)", (1024, 250_000), (1,), "f32"),
+    ("f16 [1024,250000] sum(1)", (1024, 250_000), (1,), "f16"),
+    ("f32 [16384,16000] sum(1)", (16384, 16_000), (1,), "f32"),
+    ("f32 [262144,1024] sum(1)", (262144, 1024), (1,), "f32"),
+    ("f32 [1000000,256] sum(1)", (1_000_000, 256), (1,), "f32"),
+    ("f32 [8000000,32] sum(1)", (8_000_000, 32), (1,), "f32"),
+    ("f32 [4000000,64] sum(0)", (4_000_000, 64), (0,), "f32"),
+)
+
+
+def solo_reduce_case(label, shape, axes, dt):
+    """builder._reduce_operand (the reduction stage of einsum(...,
+    reduce_solo_axes=True)) on one operand; roof = bytes read at 8 TB/s."""
+    import torch
+
+    info = {}
+
+    def prepare(dev):
+        from pto_einsum.builder import _reduce_operand
+
+        subs = "ab"
+        solo = "".join(subs[i] for i in axes)
+        g = torch.Generator().manual_seed(17)
+        x = torch.randn(shape, generator=g).to(torch.float16 if dt == "f16" else torch.float32).to(dev)
+        info["bytes"] = x.numel() * x.element_size()
+
+        def call(x):
+            _reduce_operand(x, subs, solo)
+
+        return call, (x,), info["bytes"]
+
+    def finish(ms, operands, nsets):
+        gbs = info["bytes"] / (ms * 1e-3) / 1e9
+        log(f"bench: solo reduce {label} {ms * 1e3:.1f} us  {gbs:.0f} GB/s  hbm {gbs / PEAK_HBM_GBS * 100:.1f}%")
+        return dict(reduce=label, dtype=dt, us=round(ms * 1e3, 2), gbs=round(gbs, 1), roof="hbm",
+                    frac=round(gbs / PEAK_HBM_GBS, 4), sets=nsets)
+
+    name = "R." + "x".join(str(n) for n in shape) + ".sum" + "".join(str(a) for a in axes) + "." + dt
+    return Case(name, prepare, finish)
+
+
 def gdn_cases():
     import torch
 
@@ -469,7 +514,8 @@ def all_cases():
               + [chain_case(False), chain_case(True)],
               "transposes": [transpose_case(*t) for t in transpose_list()],
               "large_f16": large_f16_cases(),
-              "gdn": gdn_cases()}
+              "gdn": gdn_cases(),
+              "solo_reduce": [solo_reduce_case(*r) for r in SOLO_REDUCE]}
     return groups
 
 
@@ -708,7 +754,7 @@ def main():
 
     rows = {k: [] for k in groups if k != "headline"}
     if not args.no_configs:
-        for grp in ("per_config", "transposes", "large_f16", "gdn"):
+        for grp in ("per_config", "transposes", "large_f16", "gdn", "solo_reduce"):
             for case in groups[grp]:
                 rows[grp].append(measure(case, dev, args.steps, args.warmup))
         pc = rows["per_config"]
