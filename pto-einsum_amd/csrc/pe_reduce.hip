@@ -223,6 +223,28 @@ __global__ __launch_bounds__(256) void reduce_tree_kernel(const float* ws, float
     }
 }
 
+// No reduced axis over one contiguous, 16-byte aligned run: a plain
+// conversion, VEC elements per lane (each +0 + x, as the order prescribes
+// for a one-term sum, so -0 becomes +0 exactly as on the general path).
+template <typename E, int VEC>
+__global__ __launch_bounds__(256) void convert_kernel(const typename E::T* __restrict__ src, float* __restrict__ dst,
+                                                       int64_t n) {
+    using Vec = typename GroupOf<typename E::T, VEC>::type;
+    const int64_t nv = n / VEC;
+    const int64_t step = int64_t(gridDim.x) * 256;
+    for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < nv; i += step) {
+        const Vec x = *reinterpret_cast<const Vec*>(src + i * VEC);
+#pragma unroll
+        for (int v = 0; v < VEC; v += 4) {
+            const f32x4 w = {0.0f + E::to_f32(x[v]), 0.0f + E::to_f32(x[v + 1]), 0.0f + E::to_f32(x[v + 2]),
+                             0.0f + E::to_f32(x[v + 3])};
+            *reinterpret_cast<f32x4*>(dst + i * VEC + v) = w;
+        }
+    }
+    for (int64_t i = nv * VEC + int64_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += step)
+        dst[i] = 0.0f + E::to_f32(src[i]);
+}
+
 __global__ __launch_bounds__(256) void zero_kernel(float* dst, int64_t n) {
     for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += int64_t(gridDim.x) * 256) dst[i] = 0.0f;
 }
@@ -269,7 +291,7 @@ int merge_axes(const int64_t* shape, const int64_t* stride, int n, int64_t* msha
 
 struct RedPlan {
     RedArgs a;
-    int mode;      // 0: zero fill (no terms), 1: row, 2: column
+    int mode;      // 0: zero fill (no terms), 1: row, 2: column, 3: contiguous conversion
     int V, L;
     int64_t ngroups;  // column mode: waves of outputs per chunk
 };
@@ -304,6 +326,13 @@ RedPlan plan_reduce(const pe_reduce_desc& d, const void* src) {
         const int64_t by_waves = ceil_div(kTargetWaves * (64 / p.L), a.nout);
         const int64_t by_len = std::max<int64_t>(1, a.G / (int64_t(p.L) * 8));  // each lane at least 8 groups
         a.C = std::max<int64_t>(1, std::min<int64_t>({by_waves, by_len, kMaxChunks}));
+    } else if (a.nred == 0 && a.nkeep <= 1 && (a.nkeep == 0 || a.keep_stride[0] == 1) && aligned(src, 16)) {
+        // Nothing to sum over one contiguous run: the conversion path (a
+        // one-term sum, V = L = C = 1).
+        p.mode = 3;
+        p.V = p.L = 1;
+        a.G = 1;
+        a.C = 1;
     } else {
         p.mode = 2;
         p.V = p.L = 1;
@@ -364,6 +393,23 @@ extern "C" int pe_reduce_axes(const pe_reduce_desc* d, const void* src, float* d
         a.ws = static_cast<float*>(ws);
     }
     const bool f16 = d->dtype == PE_F16;
+    if (p.mode == 3 && !aligned(dst, 16)) {
+        // The same one-term sums through the lane-per-output path.
+        p.mode = 2;
+        p.ngroups = ceil_div(a.nout, int64_t(64));
+    }
+    if (p.mode == 3) {
+        const int64_t nvec = ceil_div(a.nout, int64_t(8));
+        const int grid = int(std::max<int64_t>(1, std::min<int64_t>(ceil_div(nvec, 256), int64_t(cus) * 16)));
+        if (f16)
+            hipLaunchKernelGGL((convert_kernel<F16, 8>), dim3(grid), dim3(256), 0, s,
+                               static_cast<const _Float16*>(src), dst, a.nout);
+        else
+            hipLaunchKernelGGL((convert_kernel<F32, 4>), dim3(grid), dim3(256), 0, s, static_cast<const float*>(src),
+                               dst, a.nout);
+        PE_CHECK_HIP(hipGetLastError());
+        return PE_OK;
+    }
     if (p.mode == 1) {
         const int64_t blocks = ceil_div(a.nout * a.C * p.L, int64_t(256));
         if (blocks >= (int64_t(1) << 31)) return fail(PE_ERR_UNSUPPORTED, "reduce_axes: too many outputs");

@@ -45,6 +45,8 @@ CASES = [
     ((5, 7, 9), (0, 2), "", "col"),              # two reduced runs: odometer
     ((6, 33), (1,), "t", "col"),
     ((4, 3), (), "", "col"),                     # conversion only
+    ((3000, 333), (), "", "col"),                # conversion of a contiguous run (vector path)
+    ((300, 5), (), "t", "col"),                  # conversion of a strided view
     ((3, 0, 2), (1,), "", None),                 # no terms: +0
     ((3, 70001), (1,), "", "row"),               # few outputs, chunked, partial last group
     ((2, 37, 300), (1, 2), "", "row"),           # two axes merging into one run
@@ -167,3 +169,27 @@ def test_reduce_axes_validation():
         rc = lib.pe_reduce_axes(ctypes.byref(d), ctypes.c_void_p(big.data_ptr()), ctypes.c_void_p(out.data_ptr()),
                                 ctypes.c_void_p(ws), nb, st)
         assert rc == -4 and "workspace" in runtime.last_error()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16], ids=["f32", "f16"])
+def test_conversion_is_a_one_term_sum(dtype):
+    """No reduced axis: every output is +0 + x (so -0 becomes +0), on the
+    vector path (contiguous source, aligned destination) and on the
+    lane-per-output path (an unaligned destination through the C ABI)."""
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(1003, generator=g).to(dtype)
+    x[::7] = -0.0
+    x[1] = float("inf")
+    want = (torch.zeros(1003) + x.float()).numpy()
+    xd = x.cuda()
+    d = reduce_desc(xd, ())
+    lib = abi.bind()
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    buf = torch.full((1003 + 4,), float("nan"), device="cuda")
+    for off in (0, 1):  # dst 16-byte aligned, then 4 bytes past that
+        dst = buf[off:off + 1003]
+        rc = lib.pe_reduce_axes(ctypes.byref(d), ctypes.c_void_p(xd.data_ptr()), ctypes.c_void_p(dst.data_ptr()),
+                                ctypes.c_void_p(None), 0, st)
+        assert rc == 0, runtime.last_error()
+        got = dst.cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
