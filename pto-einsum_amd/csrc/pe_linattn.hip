@@ -33,8 +33,10 @@
 //      pairing lane half h with s = 8*(j/4) + 4*h + j%4, from a float32
 //      transposed V tile.
 //
-// Blocks of 32 t x 32 s whose mask is zero everywhere are skipped: their
-// contribution is exactly +-0 for finite operands.  The s axis is split over
+// Blocks of 32 t x 32 s whose mask is zero everywhere are skipped when the q,
+// k and v values they would read are finite: their contribution is then
+// exactly +-0 (with an inf or a NaN among them the block is computed, so the
+// result carries the NaN the chain of einsums would).  The s axis is split over
 // blocks for parallelism; partial outputs are summed in split order by the
 // GEMM's deterministic reduction, so results are run-to-run identical.
 //
@@ -145,6 +147,39 @@ __device__ __forceinline__ V zero_unless(bool keep, V x) {
     return keep ? x : V{};
 }
 
+// Non-finite tests (an infinity or a NaN: all exponent bits set) on raw
+// bits.  nf_bits returns a value that is nonzero when some element of x is
+// non-finite: float32 elements test their exponent directly; float16 elements
+// are tested two per 32-bit word, the exponent of each half plus 1 reaching
+// that half's bit 15 exactly when it was all ones.
+__device__ __forceinline__ uint32_t nf_word16(uint32_t w) {
+    return ((w & 0x7c007c00u) + 0x04000400u) & 0x80008000u;
+}
+__device__ __forceinline__ uint32_t nf_word32(uint32_t w) {
+    return ((w & 0x7f800000u) + 0x00800000u) & 0x80000000u;
+}
+template <typename V>
+__device__ __forceinline__ uint32_t nf_bits(const V& x) {
+    static_assert(sizeof(V) % 4 == 0 || sizeof(V) == 2, "whole words or one float16");
+    if constexpr (sizeof(V) == 2) {
+        return nf_word16(uint32_t(__builtin_bit_cast(uint16_t, x)));
+    } else {
+        constexpr int NW = sizeof(V) / 4;
+        struct Words {
+            uint32_t w[NW];
+        };
+        const Words ws = __builtin_bit_cast(Words, x);
+        const bool f16 = sizeof(x) / sizeof(x[0]) == 2 * NW;
+        uint32_t r = 0;
+#pragma unroll
+        for (int i = 0; i < NW; ++i) r |= f16 ? nf_word16(ws.w[i]) : nf_word32(ws.w[i]);
+        return r;
+    }
+}
+__device__ __forceinline__ uint32_t nf_bits(const float& x) {
+    return nf_word32(__builtin_bit_cast(uint32_t, x));
+}
+
 // K tile of one s step in LDS: kSB rows of COLS elements at a padded pitch
 // that keeps the fragment reads conflict-free and 16-byte rows aligned.
 // Loaded cooperatively in 16-byte chunks.
@@ -180,6 +215,7 @@ __global__ __launch_bounds__(kThreadsLA, 8 / kWaves) void linattn_kernel(LinAttn
     using VTile = std::conditional_t<PV32, VTileF32, VTileSplit<NV>>;
     __shared__ __attribute__((aligned(16))) VTile vt[2];                     // V tile, transposed: [p][s]
     __shared__ __attribute__((aligned(16))) T kt[2][kSB * KT::PITCH];       // K tile: [s][n]
+    __shared__ int nf_step[2];  // per stage: s offset of the last step that staged an inf or NaN
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -200,6 +236,14 @@ __global__ __launch_bounds__(kThreadsLA, 8 / kWaves) void linattn_kernel(LinAttn
         const bool ok = n < a.NP;
         qf[kk] = zero_unless(ok, *reinterpret_cast<const typename F::type*>(qrow + (ok ? n : 0)));
     }
+    // A 32x32 block whose mask is zero contributes exactly +-0 only when its q,
+    // k and v values are finite (inf * 0 and NaN give NaN in the chain of
+    // einsums): such blocks are computed, not skipped.  The wave's q rows are
+    // checked once; k and v per step as they are staged.
+    uint32_t q_nf = 0;
+#pragma unroll
+    for (int kk = 0; kk < NSTEPS; ++kk) q_nf |= nf_bits(qf[kk]);
+    const bool wave_q_nf = __any(q_nf != 0u);
 
     f32x16 acc[4];
 #pragma unroll
@@ -312,13 +356,21 @@ __global__ __launch_bounds__(kThreadsLA, 8 / kWaves) void linattn_kernel(LinAttn
         // past S or N.
         const bool full = sb + kSB <= a.S;
         float mv[16];
+        // Non-finite k / v values this thread stages: k words tested on their
+        // bits; v values through vz = fma(v, 0, vz), which stays +0 for finite
+        // v and becomes NaN after any inf or NaN (one instruction per value).
+        uint32_t kv_nf = 0;
+        float vz = 0.0f;
         if (full) {
             commit_v(stage, [&](int i) { return float(P.v[i]); });
 #pragma unroll
+            for (int i = 0; i < VROWS; ++i) vz = __builtin_fmaf(float(P.v[i]), 0.0f, vz);
+#pragma unroll
             for (int i = 0; i < KT::PER_THREAD; ++i) {
                 const int c = tid + kThreadsLA * i;
-                *reinterpret_cast<KChunk*>(&kt[stage][(c / KT::CPR) * KT::PITCH + (c % KT::CPR) * KT::VEC]) =
-                    k_all_cols ? P.k[i] : zero_unless(kcol_ok[i], P.k[i]);
+                const KChunk kc = k_all_cols ? P.k[i] : zero_unless(kcol_ok[i], P.k[i]);
+                kv_nf |= nf_bits(kc);
+                *reinterpret_cast<KChunk*>(&kt[stage][(c / KT::CPR) * KT::PITCH + (c % KT::CPR) * KT::VEC]) = kc;
             }
 #pragma unroll
             for (int q = 0; q < 4; ++q)
@@ -327,11 +379,14 @@ __global__ __launch_bounds__(kThreadsLA, 8 / kWaves) void linattn_kernel(LinAttn
         } else {
             commit_v(stage, [&](int i) { return sb + vs0 + i < a.S ? float(P.v[i]) : 0.0f; });
 #pragma unroll
+            for (int i = 0; i < VROWS; ++i) vz = __builtin_fmaf(sb + vs0 + i < a.S ? float(P.v[i]) : 0.0f, 0.0f, vz);
+#pragma unroll
             for (int i = 0; i < KT::PER_THREAD; ++i) {
                 const int c = tid + kThreadsLA * i;
                 const bool ok = sb + c / KT::CPR < a.S && kcol_ok[i];
-                *reinterpret_cast<KChunk*>(&kt[stage][(c / KT::CPR) * KT::PITCH + (c % KT::CPR) * KT::VEC]) =
-                    zero_unless(ok, P.k[i]);
+                const KChunk kc = zero_unless(ok, P.k[i]);
+                kv_nf |= nf_bits(kc);
+                *reinterpret_cast<KChunk*>(&kt[stage][(c / KT::CPR) * KT::PITCH + (c % KT::CPR) * KT::VEC]) = kc;
             }
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
@@ -340,6 +395,12 @@ __global__ __launch_bounds__(kThreadsLA, 8 / kWaves) void linattn_kernel(LinAttn
                 for (int i = 0; i < 4; ++i) mv[4 * q + i] = ok ? float(P.m[q][i]) : 0.0f;
             }
         }
+        // A wave that stages an inf or NaN marks the step (its s offset) in
+        // the stage's flag, read after the barrier (and after the next
+        // step's loads are issued) by the waves whose mask block is zero.
+        // Marks never need clearing: each step writes its own s offset, and
+        // the slot is rewritten two steps later, after every wave read it.
+        if (__any(kv_nf != 0u || vz != 0.0f) && lane == 0) nf_step[stage] = sb;
         __syncthreads();
         if (sb + kSB < s_end) prefetch(P, sb + kSB);
 
@@ -347,7 +408,7 @@ __global__ __launch_bounds__(kThreadsLA, 8 / kWaves) void linattn_kernel(LinAttn
         uint32_t mbits = 0;
 #pragma unroll
         for (int r = 0; r < 16; ++r) mbits |= __builtin_bit_cast(uint32_t, mv[r]);
-        if (__any((mbits << 1) != 0u)) {
+        if (__any((mbits << 1) != 0u) || wave_q_nf || nf_step[stage] == sb) {
             // 1. S^T block: rows s (this lane: 16 of them), column t = l32.
             //    float16: one accumulation chain (dependent 32x32 MFMAs issue
             //    back to back); float32 (64 k steps): two, even / odd.
@@ -420,6 +481,8 @@ __global__ __launch_bounds__(kThreadsLA, 8 / kWaves) void linattn_kernel(LinAttn
 
     // (A deeper register prefetch, two steps ahead, measured no faster on
     // config 5 and spilled in the float32-q/k instantiations.)
+    if (tid < 2) nf_step[tid] = -1;  // no step yet (s offsets are >= 0)
+    __syncthreads();
     Pre pre;
     if (s_begin < s_end) prefetch(pre, s_begin);
     for (int sb = s_begin, stage = 0; sb < s_end; sb += kSB, stage ^= 1) step(pre, sb, stage);

@@ -197,3 +197,31 @@ def test_c_abi_misaligned_operands_use_the_workspace():
     rc = lib.pe_linear_attention(ctypes.byref(d), *args[:5], args[5], small + (1 << 20), st)
     assert rc == 0, runtime.last_error()
     check(out.cpu().numpy(), _want(q.cpu(), k.cpu(), v.cpu(), m.cpu()), False, 2e-3, "misaligned q")
+
+
+@pytest.mark.parametrize("where", ["k", "v", "q"])
+@pytest.mark.parametrize("precise", [False, True], ids=["split_pv", "f32_pv"])
+def test_non_finite_operands_reach_masked_blocks(where, precise):
+    """The chain of einsums turns an inf or NaN under a zero mask value into
+    NaN (inf * 0); blocks whose mask is zero are skipped only when their
+    q, k and v are finite, so the same outputs come out non-finite."""
+    g = torch.Generator().manual_seed(13)
+    T, S, N, P = 160, 160, 64, 96
+    q = (torch.randn(T, N, generator=g) * N ** -0.5).half()
+    k = (torch.randn(S, N, generator=g) * N ** -0.5).half()
+    v = torch.randn(S, P, generator=g).half()
+    m = _decay(S, 0.97)[:T]           # causal: m[t, s] = 0 for s > t
+    if where == "k":
+        k[150, 3] = float("inf")      # row s = 150 lies under a zero mask for t < 150
+    elif where == "v":
+        v[140, 7] = float("inf")
+    else:
+        q[10, 0] = float("nan")
+    got = _run(q, k, v, m, precise=precise).numpy()
+    want = _want(q, k, v, m)
+    assert np.array_equal(np.isfinite(got), np.isfinite(want))
+    assert not np.isfinite(want).all()
+    fin = np.isfinite(want)
+    if fin.any():
+        err = float(np.abs(got[fin] - want[fin]).max())
+        assert err <= 2e-3 * max(1.0, float(np.abs(want[fin]).max()))
