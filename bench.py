@@ -178,6 +178,55 @@ def copy_probe():
     print(json.dumps({"copy_probe_bytes_each_way": n * 4, "launches": 5}))
 
 
+def attainable(dev):
+    """Attainable peaks on this device, measured with kernels of this build:
+    a 1 GiB float32 copy (the permutation launcher with the identity; cold,
+    as 1 GiB exceeds the Infinity Cache) and the MFMA probe (no memory
+    traffic; float16 on random and on constant operands, float32 on random
+    ones -- the clock follows the operands' bit activity)."""
+    import torch
+
+    from pto_einsum import abi, launch
+
+    lib = abi.bind()
+    st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+    def timed(fn, reps=5):
+        for _ in range(2):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps * 1e-3  # seconds per call
+
+    n = 1 << 28
+    src = torch.ones(n, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    d = abi.permute_desc(launch.PermuteDesc(4, [n], [1], n))
+
+    def copy():
+        rc = lib.pe_permute(ctypes.byref(d), ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(dst.data_ptr()), st)
+        if rc != 0:
+            raise RuntimeError("copy probe failed")
+
+    out = {"copy_gbs": round(2 * n * 4 / timed(copy) / 1e9, 1)}
+    del src, dst
+    buf = torch.empty(int(lib.pe_probe_out_len()), dtype=torch.float32, device=dev)
+    for name, dt, rnd, iters in (("mfma_f16_random_tflops", 1, 1, 2000), ("mfma_f16_constant_tflops", 1, 0, 2000),
+                                 ("mfma_f32_random_tflops", 0, 1, 2000)):
+        def probe():
+            rc = lib.pe_probe_mfma(dt, rnd, iters, ctypes.c_void_p(buf.data_ptr()), buf.numel(), st)
+            if rc != 0:
+                raise RuntimeError("mfma probe failed")
+        out[name] = round(int(lib.pe_probe_mfma_flops(dt, iters)) / timed(probe) / 1e12, 1)
+    log(f"bench: attainable {out}")
+    return out
+
+
 def traffic_from_profile():
     path = os.path.join(ROOT, "profiles", "gemm_f32_config2_traffic.json")
     try:
@@ -753,6 +802,7 @@ def main():
     torch.cuda.empty_cache()
 
     rows = {k: [] for k in groups if k != "headline"}
+    rows["attainable"] = attainable(dev)
     if not args.no_configs:
         for grp in ("per_config", "transposes", "large_f16", "gdn", "solo_reduce"):
             for case in groups[grp]:

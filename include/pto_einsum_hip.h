@@ -217,6 +217,16 @@ const char* pe_last_error(void);        /* message for the calling thread's last
 int pe_device_cu_count(void);           /* compute units of the current device */
 const char* pe_version(void);
 
+/* Attainable-peak probe for the measurement harness (no counterpart in the
+ * reference): MFMA throughput with no memory traffic, v_mfma_f32_32x32x16_f16
+ * (dtype PE_F16) or v_mfma_f32_32x32x2_f32 (PE_F32), on random (random != 0)
+ * or constant operands; the clock, and so the rate, depends on the operands'
+ * bit activity.  out receives one float per lane (pe_probe_out_len()
+ * floats); pe_probe_mfma_flops gives the flops one call performs. */
+int pe_probe_mfma(int dtype, int random, int64_t iters, float* out, int64_t out_len, void* stream);
+int64_t pe_probe_mfma_flops(int dtype, int64_t iters);
+int64_t pe_probe_out_len(void);
+
 /* ---- per-shape entry points (one JIT library per equation/shapes/dtype) ----
  * Declared here with T = void; the generated source defines them with the
  * element type of its dtype. */

@@ -144,7 +144,11 @@ def bind(lib=None):
     lib.pe_reduce_workspace_bytes.argtypes = [ctypes.POINTER(ReduceDesc)]
     lib.pe_reduce_workspace_bytes.restype = ctypes.c_int64
     lib.pe_reduce_order.argtypes = [ctypes.POINTER(ReduceDesc), vp, ctypes.POINTER(ctypes.c_int64)]
-    for f in ("pe_product", "pe_permute", "pe_gemm", "pe_einsum_exec", "pe_einsum_teardown", "pe_einsum_run",
+    lib.pe_probe_mfma.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int64, vp, ctypes.c_int64, vp]
+    lib.pe_probe_mfma_flops.argtypes = [ctypes.c_int, ctypes.c_int64]
+    lib.pe_probe_mfma_flops.restype = ctypes.c_int64
+    lib.pe_probe_out_len.restype = ctypes.c_int64
+    for f in ("pe_product", "pe_permute", "pe_gemm", "pe_einsum_exec", "pe_einsum_teardown", "pe_einsum_run", "pe_probe_mfma",
               "pe_einsum_exec_noalloc", "pe_linear_attention", "pe_reduce_axes", "pe_reduce_order"):
         getattr(lib, f).restype = ctypes.c_int
     return lib
