@@ -280,3 +280,26 @@ def test_gemm_grids_of_wide_tiles(layout_a, layout_b, dtype, nbatch, M, N, K):
     scale = float(want.abs().max())
     rtol = 1e-4 if dtype == torch.float32 else 2e-3
     assert float((got.double() - want).abs().max()) <= rtol * scale
+
+
+def test_mfma_probe_runs_and_validates():
+    """The attainable-peak probe: finite per-lane sums, positive flops, and
+    the argument checks of its C entry point."""
+    import ctypes
+
+    from pto_einsum import abi, runtime
+
+    lib = abi.bind()
+    n = int(lib.pe_probe_out_len())
+    out = torch.full((n,), float("nan"), device="cuda")
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for dt in (0, 1):
+        for rnd in (0, 1):
+            rc = lib.pe_probe_mfma(dt, rnd, 3, ctypes.c_void_p(out.data_ptr()), n, st)
+            assert rc == 0, runtime.last_error()
+            torch.cuda.synchronize()
+            assert bool(torch.isfinite(out).all())
+        assert int(lib.pe_probe_mfma_flops(dt, 3)) > 0
+    assert lib.pe_probe_mfma(7, 0, 3, ctypes.c_void_p(out.data_ptr()), n, st) == -3
+    assert lib.pe_probe_mfma(1, 0, 0, ctypes.c_void_p(out.data_ptr()), n, st) == -1
+    assert lib.pe_probe_mfma(1, 0, 3, ctypes.c_void_p(out.data_ptr()), n - 1, st) == -2
