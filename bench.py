@@ -1,6 +1,6 @@
 """Benchmark of the MI355X einsum path (one JSON line on stdout).
 
-Headline workload: BASELINE config 2, the transposing batched contraction
+Headline workload: benchmark config 2, the transposing batched contraction
 ``bji,bjk->bik`` in float32 with b=16, i=1000, j=777, k=1536 (standard-normal
 inputs from a seed).  A step is one ``run_einsum_exec`` over that batch with
 operands and output resident in HBM.  ``value`` is TFLOP/s over the timed
@@ -16,7 +16,7 @@ therefore rotates through enough copies of its operands and output (at least
 has touched for over 768 MB of traffic: the figures are HBM figures, not
 cache figures.  The headline steps rotate the same way.
 
-``per_config`` adds every other BASELINE equation at full size with its own
+``per_config`` adds every other benchmark equation at full size with its own
 binding roof (HBM bytes or MFMA flops).  Those kernels run for tens of
 microseconds, less than one Python-level call costs, so the rotation's calls
 are captured once in a HIP graph and the graph is replayed between two
@@ -258,7 +258,7 @@ def decay(t, gamma):
 
 
 def config_list():
-    """BASELINE configs other than the headline: (name, equation, operand
+    """benchmark configs other than the headline: (name, equation, operand
     generator, roof dtype)."""
     import torch
 
@@ -283,7 +283,7 @@ def config_list():
 
 def transpose_list():
     """The reference recipe's standalone operand / output transposes (Phase A
-    and Phase C of pto_einsum.h:52-177) for the BASELINE contractions that
+    and Phase C of pto_einsum.h:52-177) for the benchmark contractions that
     have them, run through the per-shape library's run_transpose_* entry
     points: (label, equation, operand shapes, dtype, entry point)."""
     import torch
@@ -430,7 +430,7 @@ T5, N5 = 4096, 128
 
 
 def chain_case(precise):
-    """BASELINE config 5's linear-attention chain in one fused launch
+    """benchmark config 5's linear-attention chain in one fused launch
     (pto_einsum.linear_attention): q, k float16 normal(0, 1/sqrt(128)), v
     float16 normal(0, 1), the causal decay mask gamma^(t-s), gamma = 0.995,
     in float32; t = s = 4096, n = p = 128.  The default launch computes P.V

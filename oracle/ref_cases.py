@@ -11,7 +11,7 @@ exactly the routes the reference exercises:
   these are C=1 matmuls, builder.py:375-376);
 * ``CHAIN_CASES``      -- the linear-attention steps of
   tests/test_llm_ops.py:81-107 at T=S in {96, 320};
-* ``CONFIG_CASES``     -- the BASELINE equations at reduced sizes, plus edge
+* ``CONFIG_CASES``     -- the benchmark equations at reduced sizes, plus edge
   shapes (size-1 axes, scalar output, multi-axis contraction order);
 * ``BENCH_SAMPLE``     -- the CPU baseline bench.py times: the whole of
   config 2 (``bji,bjk->bik``, b=16, j=777, i=1000, k=1536).
@@ -103,7 +103,7 @@ CHAIN_CASES = [
 ]
 
 CONFIG_CASES = [
-    # BASELINE equations at reduced sizes
+    # benchmark equations at reduced sizes
     ("bji,bjk->bik", (2, 77, 100), (2, 77, 153)),
     ("bshd,bthd->bsht", (2, 48, 4, 32), (2, 40, 4, 32)),
     ("ts,ts->ts", (128, 96), (128, 96)),

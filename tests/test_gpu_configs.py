@@ -1,4 +1,4 @@
-"""BASELINE configurations at their full sizes on the GPU.
+"""The benchmark configurations at their full sizes on the GPU.
 
 Products (4a, 4b, 5.2, RoPE) are compared with the oracle over every output
 element, bit for bit.  Contractions (1, 2, 3, 5.1, 5.3) are compared with the

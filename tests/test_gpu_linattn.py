@@ -1,7 +1,7 @@
 """Fused linear-attention chain on the GPU against the oracle's three-step
 chain (float32 intermediates).  The reference covers the chain with
 tests/test_llm_ops.py:81-107 (T = S in {96, 320}, N = 64, P = 128, a
-lower-triangular ones mask, both dtypes); these cases add BASELINE config 5's
+lower-triangular ones mask, both dtypes); these cases add benchmark config 5's
 full size with its decay mask, partial tiles in every axis, several s splits,
 float16 masks and values, dense masks and strided rows."""
 import numpy as np
@@ -125,7 +125,7 @@ def test_zero_mask_and_strided_rows():
 
 
 def test_config5_full_size():
-    """BASELINE config 5's chain at full size (t = s = 4096, n = p = 128,
+    """benchmark config 5's chain at full size (t = s = 4096, n = p = 128,
     gamma = 0.995): every element against a float64 GPU evaluation of the
     same chain, sampled rows against the oracle."""
     g = torch.Generator().manual_seed(6)

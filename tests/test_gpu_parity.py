@@ -1,7 +1,7 @@
 """GPU parity: the gfx950 path against the CPU oracle, through the public API.
 
 Case lists follow the reference's own test matrices (tests/test_einsum.py:22-129,
-tests/test_llm_ops.py:34-125) plus the BASELINE equations at reduced sizes and
+tests/test_llm_ops.py:34-125) plus the benchmark equations at reduced sizes and
 edge shapes.  Every case runs in float32 and float16.
 """
 import numpy as np

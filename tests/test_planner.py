@@ -1,4 +1,4 @@
-"""Planner restatement: recipes for the BASELINE equations derived by hand
+"""Planner restatement: recipes for the benchmark equations derived by hand
 from builder.py:185-604, the reference's codegen gate strings, its error
 contracts, and agreement with the oracle's independently written recipe."""
 import os
