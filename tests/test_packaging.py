@@ -24,6 +24,9 @@ def installed(tmp_path_factory):
     assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
     wheels = glob.glob(str(wheel_dir / "*.whl"))
     assert len(wheels) == 1 and "linux" in os.path.basename(wheels[0])
+    # The build leaves no header copy in the source package (it would shadow
+    # include/ for the in-tree JIT and go stale).
+    assert not os.path.exists(os.path.join(ROOT, "pto-einsum_amd", "pto_einsum", "include"))
     r = subprocess.run([sys.executable, "-m", "pip", "install", "--no-deps", "--no-index", "--target", str(target),
                         wheels[0]], capture_output=True, text=True, timeout=300)
     assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
