@@ -102,6 +102,15 @@ typedef struct pe_einsum_plan {
     pe_gemm_desc gemm;
     int64_t ws0_off, ws1_off, wsout_off, wsgemm_off;
     int64_t ws_bytes;                     /* total workspace bytes */
+    /* Phase ablation for timing by subtraction (the reference's
+     * EINSUM_PHASE_STOP, include/pto_einsum.h:17-29, builder.py:688-697):
+     * bit 0 skips phase A (the operand gathers), bit 1 phase B (the GEMM with
+     * its split reduction, or the product kernel), bit 2 phase C (the output
+     * permutation).  Skipped phases launch nothing and leave what they would
+     * write unwritten.  0 runs the whole plan.  The per-shape wrapper sets it
+     * from EINSUM_PHASE_STOP = N (default 3): the phases after the N-th. */
+    int32_t skip_phases;
+    int32_t reserved;                     /* must be 0 */
 } pe_einsum_plan;
 
 /* ---- core library (libpto_einsum_hip.so) ---- */

@@ -101,7 +101,10 @@ extern "C" int pe_einsum_exec(const pe_einsum_plan* p, const void* in0, const vo
                               void* ws, void* stream) {
     using namespace pe;
     if (!p) return fail(PE_ERR_INVALID, "exec: null plan");
-    if (p->route == PE_ROUTE_PRODUCT) return pe_product(&p->product, in0, in1, out, stream);
+    if (p->skip_phases < 0 || p->skip_phases > 7 || p->reserved != 0)
+        return fail(PE_ERR_INVALID, "exec: skip_phases must be in [0, 7] and reserved 0");
+    const bool run_a = !(p->skip_phases & 1), run_b = !(p->skip_phases & 2), run_c = !(p->skip_phases & 4);
+    if (p->route == PE_ROUTE_PRODUCT) return run_b ? pe_product(&p->product, in0, in1, out, stream) : PE_OK;
     if (p->route != PE_ROUTE_GEMM) return fail(PE_ERR_INVALID, "exec: unknown route");
     char* w = static_cast<char*>(ws);
     const bool staged = p->gather0 || p->gather1 || p->scatter_out;
@@ -111,19 +114,19 @@ extern "C" int pe_einsum_exec(const pe_einsum_plan* p, const void* in0, const vo
     const void* b = in1;
     int st;
     if (p->gather0) {
-        st = pe_permute(&p->perm0, in0, w + p->ws0_off, stream);
+        st = run_a ? pe_permute(&p->perm0, in0, w + p->ws0_off, stream) : PE_OK;
         if (st != PE_OK) return st;
         a = w + p->ws0_off;
     }
     if (p->gather1) {
-        st = pe_permute(&p->perm1, in1, w + p->ws1_off, stream);
+        st = run_a ? pe_permute(&p->perm1, in1, w + p->ws1_off, stream) : PE_OK;
         if (st != PE_OK) return st;
         b = w + p->ws1_off;
     }
     float* c = p->scatter_out ? reinterpret_cast<float*>(w + p->wsout_off) : out;
-    st = pe_gemm(&p->gemm, a, b, c, w ? w + gemm_ws_offset(*p) : nullptr, gws, stream);
+    st = run_b ? pe_gemm(&p->gemm, a, b, c, w ? w + gemm_ws_offset(*p) : nullptr, gws, stream) : PE_OK;
     if (st != PE_OK) return st;
-    if (p->scatter_out) {
+    if (p->scatter_out && run_c) {
         st = pe_permute(&p->perm_out, c, out, stream);
         if (st != PE_OK) return st;
     }

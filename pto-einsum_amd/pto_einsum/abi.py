@@ -45,7 +45,7 @@ class EinsumPlan(ctypes.Structure):
                 ("perm_out", PermuteDesc), ("gemm", GemmDesc),
                 ("ws0_off", ctypes.c_int64), ("ws1_off", ctypes.c_int64),
                 ("wsout_off", ctypes.c_int64), ("wsgemm_off", ctypes.c_int64),
-                ("ws_bytes", ctypes.c_int64)]
+                ("ws_bytes", ctypes.c_int64), ("skip_phases", ctypes.c_int32), ("reserved", ctypes.c_int32)]
 
 
 class LinAttnDesc(ctypes.Structure):

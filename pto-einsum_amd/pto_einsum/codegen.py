@@ -137,7 +137,9 @@ def plan_function(plan: L.LaunchPlan) -> str:
             body.append(_permute_fill("p.perm_out", plan.perm_out))
         body += [f"    p.ws0_off = {plan.ws0_off}LL;", f"    p.ws1_off = {plan.ws1_off}LL;",
                  f"    p.wsout_off = {plan.wsout_off}LL;", f"    p.ws_bytes = {plan.ws_bytes}LL;"]
-    body += ["    return p;", "}", "static const pe_einsum_plan kPlan = make_plan();", ""]
+    body += ["    p.skip_phases = (EINSUM_PHASE_STOP < 1 ? 1 : 0) | (EINSUM_PHASE_STOP < 2 ? 2 : 0) |",
+             "                    (EINSUM_PHASE_STOP < 3 ? 4 : 0);",
+             "    return p;", "}", "static const pe_einsum_plan kPlan = make_plan();", ""]
     return "\n".join(body)
 
 
@@ -165,6 +167,12 @@ def gpu_source(equation: str, shapes, dtype_name: str, recipe: Dict, exec_shapes
         "#define PE_NO_PER_SHAPE_DECLS",
         '#include "pto_einsum_hip.h"',
         "#include <string.h>",
+        "",
+        "// Phase ablation (EINSUM_EXTRA_DEFINES=-DEINSUM_PHASE_STOP=N): phases after",
+        "// the N-th launch nothing (0: none, 1: operand gathers, 2: + GEMM, 3: all).",
+        "#ifndef EINSUM_PHASE_STOP",
+        "#define EINSUM_PHASE_STOP 3",
+        "#endif",
         "",
     ]
     configs = []

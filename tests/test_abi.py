@@ -92,6 +92,7 @@ int main() {
   OFF(pe_linattn_desc, m_numel); OFF(pe_linattn_desc, precise);
   OFF(pe_product_desc, b_numel); OFF(pe_permute_desc, src_numel); OFF(pe_gemm_desc, M);
   OFF(pe_gemm_desc, c_numel); OFF(pe_einsum_plan, gemm); OFF(pe_einsum_plan, ws_bytes);
+  OFF(pe_einsum_plan, skip_phases);
   printf("pe_reduce_desc %zu\n", sizeof(pe_reduce_desc));
   OFF(pe_reduce_desc, red_stride); OFF(pe_reduce_desc, src_numel);
   return 0;
@@ -116,6 +117,7 @@ def test_ctypes_struct_layout_matches_c(tmp_path):
     assert int(vals["pe_gemm_desc.c_numel"]) == abi.GemmDesc.c_numel.offset
     assert int(vals["pe_einsum_plan.gemm"]) == abi.EinsumPlan.gemm.offset
     assert int(vals["pe_einsum_plan.ws_bytes"]) == abi.EinsumPlan.ws_bytes.offset
+    assert int(vals["pe_einsum_plan.skip_phases"]) == abi.EinsumPlan.skip_phases.offset
     assert int(vals["pe_linattn_desc"]) == ctypes.sizeof(abi.LinAttnDesc)
     assert int(vals["pe_linattn_desc.m_numel"]) == abi.LinAttnDesc.m_numel.offset
     assert int(vals["pe_linattn_desc.precise"]) == abi.LinAttnDesc.precise.offset
@@ -154,3 +156,25 @@ def test_noalloc_rejects_oversized_plan_without_launch():
     plan = abi.einsum_plan(b.launch_plan)
     assert lib.pe_einsum_exec_noalloc(ctypes.byref(plan), None, None, None, None) == -4
     assert b"scratch limit" in lib.pe_last_error()
+
+
+@pytest.mark.parametrize("stop,skip", [(None, 0), (3, 0), (2, 4), (1, 6), (0, 7)])
+def test_phase_stop_define_reaches_the_plan(stop, skip, tmp_path):
+    """EINSUM_PHASE_STOP (passed through EINSUM_EXTRA_DEFINES, as in the
+    reference's builder.py:688-697) sets the plan's skip_phases in the
+    per-shape source: the phases after the N-th are skipped."""
+    b = EinsumBuilder("acb,cd->abd", [(48, 64, 6), (64, 72)], torch.float32)
+    b.parse_equation()
+    b.generate_code()
+    assert "#define EINSUM_PHASE_STOP 3" in b.cpp_code
+    src = tmp_path / "probe.cpp"
+    src.write_text(b.cpp_code + '\n#include <cstdio>\nint main() { printf("%d\\n", kPlan.skip_phases); return 0; }\n')
+    exe = tmp_path / "probe"
+    libdir = os.path.dirname(runtime.core_library_path())
+    cmd = ["g++", "-std=c++17", "-I", os.path.dirname(HEADER), str(src), "-o", str(exe),
+           "-L", libdir, "-lpto_einsum_hip", "-Wl,-rpath," + libdir]
+    if stop is not None:
+        cmd.insert(1, f"-DEINSUM_PHASE_STOP={stop}")
+    subprocess.run(cmd, check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout
+    assert int(out) == skip

@@ -134,6 +134,55 @@ def test_free_axes_made_batch_on_gpu(eq, s0, s1, dtype, build_dir):
     check(got, want, False, RTOL[dtype], eq)
 
 
+@pytest.mark.parametrize("eq,s0,s1", [("acb,cd->abd", (48, 64, 6), (64, 72)),    # gathers in0
+                                      ("abc,cd->adb", (64, 6, 96), (96, 80)),    # stages the result
+                                      ("bsd,d->bsd", (2, 16, 64), (64,))])       # one product launch
+def test_phase_skip_leaves_skipped_outputs_unwritten(eq, s0, s1):
+    """pe_einsum_exec with skip_phases (the EINSUM_PHASE_STOP ablation): the
+    whole plan (0) gives the einsum, and a skipped phase that would write the
+    output leaves it as it was (NaN sentinel); skipping only a phase the plan
+    does not have changes nothing."""
+    from parity_util import make_inputs
+
+    lib = abi.bind()
+    b = EinsumBuilder(eq, [s0, s1], torch.float32)
+    b.parse_equation()
+    b.generate_code()
+    lp = b.launch_plan
+    plan = abi.einsum_plan(lp)
+    x, y = make_inputs(eq, s0, s1, torch.float32)
+    x, y = x.cuda(), y.cuda()
+    if b._swap_operands:
+        x, y = y, x
+    ws = lib.pe_einsum_setup(ctypes.byref(plan), _stream())
+    assert ws or plan.ws_bytes == 0, runtime.last_error()
+
+    def run(skip):
+        plan.skip_phases = skip
+        out = torch.full(b.recipe["out_shape"], float("nan"), device="cuda")
+        print(f"phase skip {skip}: {eq} {s0} {s1}", flush=True)
+        rc = lib.pe_einsum_exec(ctypes.byref(plan), _ptr(x), _ptr(y), _ptr(out), ctypes.c_void_p(ws), _stream())
+        assert rc == 0, runtime.last_error()
+        torch.cuda.synchronize()
+        return out
+
+    full = run(0)
+    want = oracle.einsum(eq, *(t.float().cpu().numpy() for t in ((y, x) if b._swap_operands else (x, y))))
+    check(full.cpu().numpy(), want, False, 1e-4, eq)
+    assert bool(run(7).isnan().all())
+    if lp.route == launch.ROUTE_PRODUCT or not lp.scatter_out:
+        assert bool(run(2).isnan().all())          # the GEMM / product writes the output
+        assert torch.equal(run(4), full)           # no output permutation to skip
+    else:
+        assert bool(run(4).isnan().all())          # the output permutation writes it
+    if lp.route != launch.ROUTE_PRODUCT and not (lp.gather0 or lp.gather1):
+        assert torch.equal(run(1), full)           # no gather to skip
+    plan.skip_phases = 8
+    assert lib.pe_einsum_exec(ctypes.byref(plan), _ptr(x), _ptr(y), _ptr(full), ctypes.c_void_p(ws), _stream()) != 0
+    if ws:
+        assert lib.pe_einsum_teardown(ctypes.c_void_p(ws)) == 0
+
+
 def _gemm_direct(a, b, M, N, K, a_ms, a_ks, b_ks, b_ns, dtype_code, tile=0, split_k=0, nbatch=2):
     """C[bt] = A[bt] @ B[bt] through pe_gemm with explicit strides; A and B are
     flat device buffers holding `nbatch` operands each."""
