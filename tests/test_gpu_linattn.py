@@ -119,6 +119,11 @@ def test_zero_mask_and_strided_rows():
     m = torch.zeros(T, S)
     got = _run(q, k, v, m)
     assert torch.equal(got, torch.zeros(T, P))
+    # Split partials of tiles that skipped every step are not stored and are
+    # read back as +0: the sum stays +0 bit for bit (no -0).
+    for split in (2, 5):
+        got = _run(q, k, v, m, split=split)
+        assert bool((got.view(torch.int32) == 0).all())
     m[5, 7] = 1.0   # one nonzero element: only row 5 is nonzero
     got = _run(q, k, v, m)
     check(got.numpy(), _want(q, k, v, m), False, 2e-3, "single nonzero")

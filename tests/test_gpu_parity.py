@@ -58,6 +58,24 @@ def test_deterministic(eq, s0, s1, dtype, build_dir):
     builder.cleanup()
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16], ids=["f32", "f16"])
+def test_broadcast_multi_op_sequence(dtype, build_dir):
+    """tests/test_llm_ops.py:146-165: distinct broadcast builders built, run and
+    cleaned up back to back, each with the same seed, so an op that read a
+    stale buffer of the previous one (or a store still in flight) would show
+    up as a wrong result; every output is checked bit for bit against the
+    oracle (the broadcast route is exact: one product per element)."""
+    from pto_einsum import EinsumBuilder
+
+    for eq, s0, s1 in BROADCAST_CASES:
+        torch.manual_seed(0)
+        a, b = torch.rand(s0).to(dtype), torch.rand(s1).to(dtype)
+        builder = EinsumBuilder(eq, [s0, s1], dtype)
+        got = builder.build()(a.cuda(), b.cuda()).cpu().numpy()
+        check(got, oracle.einsum(eq, a.float().numpy(), b.float().numpy()), True, 0.0, f"{eq} {dtype}")
+        builder.cleanup()
+
+
 def test_builder_reuse(build_dir):
     """test_einsum.py:208-241: a runner reused with fresh data, incl. K != C."""
     from pto_einsum import EinsumBuilder
