@@ -264,19 +264,21 @@ def plan_launch(recipe: Dict, exec_eq: str, shape0, shape1, dtype_code: int) -> 
     orders: Dict[str, Tuple[str, ...]] = {}
     for _ in range(4):
         changed = False
-        for name, grp, (t1, t2) in groups:
-            live = [t for t in (t1, t2) if not staged[t]]
+        # (ta, tb: the two tensor names that carry the group; t0 / t1 stay the
+        # operands' subscripts, which the layouts below read.)
+        for name, grp, (ta, tb) in groups:
+            live = [t for t in (ta, tb) if not staged[t]]
             order = None
             if len(live) == 2:
-                for cand in _candidate_orders(grp, size, [natural[t1], natural[t2]]):
-                    if _mergeable(cand, size, natural[t1]) and _mergeable(cand, size, natural[t2]):
+                for cand in _candidate_orders(grp, size, [natural[ta], natural[tb]]):
+                    if _mergeable(cand, size, natural[ta]) and _mergeable(cand, size, natural[tb]):
                         order = cand
                         break
                 if order is None:
                     # Keep the tensor that can hold the group by itself; stage the
                     # other (output last: staging C costs a full extra pass).
-                    keep = t2 if (t2 == "C" or own_order(grp, t1) is None) and own_order(grp, t2) else t1
-                    drop = t1 if keep == t2 else t2
+                    keep = tb if (tb == "C" or own_order(grp, ta) is None) and own_order(grp, tb) else ta
+                    drop = ta if keep == tb else tb
                     staged[drop] = True
                     changed = True
                     order = own_order(grp, keep)

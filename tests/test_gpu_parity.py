@@ -76,6 +76,41 @@ def test_broadcast_multi_op_sequence(dtype, build_dir):
         builder.cleanup()
 
 
+@pytest.mark.parametrize("seed", [1, 2])
+def test_random_einsums_against_the_oracle(seed, build_dir):
+    """150 seeded random equations per seed (tests/random_einsum.py: batch,
+    free and contracted axes in random counts, sizes and orders, both dtypes,
+    a third of the operands as non-contiguous views) through the public
+    einsum against the oracle; equations with single-operand reduction axes
+    (reduce_solo_axes=True) against torch's float64 einsum."""
+    import random
+
+    from pto_einsum import einsum
+    from random_einsum import random_case
+
+    rng = random.Random(seed)
+    for i in range(150):
+        eq, s0, s1, solo = random_case(rng, solo=True, max_elems=1e6, max_work=5e7)
+        dtype = rng.choice([torch.float32, torch.float16])
+        a, b = make_inputs(eq, s0, s1, dtype)
+        ga, gb = a.cuda(), b.cuda()
+        if ga.dim() >= 2 and rng.random() < 0.33:
+            ga = ga.t().contiguous().t() if ga.dim() == 2 else ga.transpose(0, -1).contiguous().transpose(0, -1)
+        if gb.dim() >= 2 and rng.random() < 0.33:
+            gb = gb.t().contiguous().t() if gb.dim() == 2 else gb.transpose(0, -1).contiguous().transpose(0, -1)
+        what = f"random case {seed}.{i}: {eq} {s0} {s1} {dtype}{' solo' if solo else ''}"
+        print(what, flush=True)
+        got = einsum(eq, ga, gb, reduce_solo_axes=solo).cpu()
+        if solo:
+            want = torch.einsum(eq, a.double(), b.double())
+            scale = float(want.abs().max()) if want.numel() else 0.0
+            err = float((got.double() - want).abs().max()) if want.numel() else 0.0
+            assert err <= RTOL[dtype] * max(scale, 1e-30), f"{what}: err {err:.3e} scale {scale:.3e}"
+        else:
+            want = oracle.einsum(eq, a.float().numpy(), b.float().numpy())
+            check(got.numpy(), want, contraction_size(eq, s0, s1) <= 1, RTOL[dtype], what)
+
+
 def test_builder_reuse(build_dir):
     """test_einsum.py:208-241: a runner reused with fresh data, incl. K != C."""
     from pto_einsum import EinsumBuilder

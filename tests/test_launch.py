@@ -32,6 +32,9 @@ EXTRA = [
     ("acb,cd->abd", (5, 7, 18), (7, 8)),       # ... split in operand 0
     ("abcd,de->bcea", (4, 5, 6, 8), (8, 24)),  # free0 {a,b,c}: {b,c} kept, a made batch
     ("bac,cdb->adb", (3, 4, 7), (7, 20, 3)),   # a true batch axis beside a promoted one
+    ("nrD,nDr->n", (33, 7, 2), (33, 2, 7)),    # operand 1 staged with a batch axis
+    ("qx,xsaq->asx", (31, 64), (64, 3, 32, 31)),
+    ("AoeEy,nymE->meAno", (2, 31, 1, 64, 64), (3, 64, 33, 64)),  # subscripts A / B / C
 ]
 CASES = EINSUM_CASES + ATTENTION_CASES + BROADCAST_CASES + CHAIN_CASES + CONFIG_CASES + EXTRA
 
@@ -127,3 +130,30 @@ def test_products_take_the_stream_route(eq, s0, s1):
     b, plan = _plan(eq, s0, s1)
     assert plan.route == launch.ROUTE_PRODUCT
     assert plan.product.add_zero == (0 if b.recipe["elementwise"] else 1)
+
+
+def test_random_plans_compute_the_einsum():
+    """600 seeded random equations (tests/random_einsum.py), single-operand
+    reduction axes summed first as einsum(reduce_solo_axes=True) does: every
+    plan, emulated in float64, gives torch's float64 einsum."""
+    import random
+
+    from pto_einsum import planner
+    from random_einsum import random_case
+
+    rng = random.Random(20261202)
+    for i in range(600):
+        eq, s0, s1, solo = random_case(rng, solo=True, max_elems=2e5, max_work=2e6)
+        g = np.random.default_rng(i)
+        x, y = g.standard_normal(s0), g.standard_normal(s1)
+        want = torch.einsum(eq, torch.from_numpy(x), torch.from_numpy(y)).numpy()
+        if solo:
+            eq, in0, in1, solo0, solo1 = planner.solo_split(eq, s0, s1)
+            x = x.sum(axis=tuple(in0.index(a) for a in solo0)) if solo0 else x
+            y = y.sum(axis=tuple(in1.index(a) for a in solo1)) if solo1 else y
+        b, plan = _plan(eq, x.shape, y.shape)
+        xe, ye = (y, x) if b._swap_operands else (x, y)
+        got = emulate(plan, xe, ye, b.recipe["out_shape"])
+        assert not np.isnan(got).any(), f"case {i} {eq}: an output element was never written"
+        scale = max(1.0, float(np.abs(want).max())) if want.size else 1.0
+        assert np.allclose(got, want, rtol=1e-9, atol=1e-9 * scale), f"case {i} {eq} {x.shape} {y.shape}"
