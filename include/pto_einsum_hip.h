@@ -187,7 +187,9 @@ typedef struct pe_reduce_desc {
 
 int pe_reduce_axes(const pe_reduce_desc* d, const void* src, float* dst, void* ws, int64_t ws_bytes,
                    void* stream);
-/* Workspace bytes pe_reduce_axes needs for d (0 when C = 1 or d is invalid). */
+/* Workspace bytes pe_reduce_axes needs for d at any source address (the larger
+ * of the 16-byte-aligned and unaligned plans; 0 when C = 1 for both, or d is
+ * invalid). */
 int64_t pe_reduce_workspace_bytes(const pe_reduce_desc* d);
 /* The (V, L, C) of the summation order above for d and a source at src (V
  * depends on src's 16-byte alignment), into order[0..2]. */

@@ -351,8 +351,16 @@ RedPlan plan_reduce(const pe_reduce_desc& d, const void* src) {
 extern "C" int64_t pe_reduce_workspace_bytes(const pe_reduce_desc* d) {
     using namespace pe;
     if (!d || validate(*d) != PE_OK) return 0;
-    const RedPlan p = plan_reduce(*d, nullptr);
-    return p.a.C > 1 ? p.a.C * p.a.nout * int64_t(sizeof(float)) : 0;
+    // No source address here, so the size covers both alignments: a base that
+    // is not 16-byte aligned takes one-element groups, hence more groups and
+    // possibly more chunks than an aligned one.  (The planner only tests the
+    // address for alignment; neither value is dereferenced.)
+    int64_t bytes = 0;
+    for (const void* src : {static_cast<const void*>(nullptr), reinterpret_cast<const void*>(uintptr_t(4))}) {
+        const RedPlan p = plan_reduce(*d, src);
+        if (p.a.C > 1) bytes = std::max<int64_t>(bytes, p.a.C * p.a.nout * int64_t(sizeof(float)));
+    }
+    return bytes;
 }
 
 extern "C" int pe_reduce_order(const pe_reduce_desc* d, const void* src, int64_t* order) {

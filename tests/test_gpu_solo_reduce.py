@@ -36,6 +36,10 @@ def _view(x: torch.Tensor, how: str) -> torch.Tensor:
         big = torch.zeros(x.shape[0], x.shape[1] + 1, dtype=x.dtype)
         big[:, 1:] = x
         return big.cuda()[:, 1:]
+    if how == "shift":    # x's values one element into a flat buffer (contiguous, base not 16-byte aligned)
+        flat = torch.zeros(x.numel() + 1, dtype=x.dtype)
+        flat[1:] = x.reshape(-1)
+        return flat.cuda()[1:].reshape(x.shape)
     return x.cuda()
 
 
@@ -59,6 +63,8 @@ CASES = [
     ((300, 8, 200), (0, 2), "", "col"),          # odometer chunks starting mid-run
     ((7, 20), (1,), "", "col"),                  # short runs go lane-per-output
     ((1000, 40), (1,), "", "row"),               # four lanes per output, 16 outputs per wave
+    ((1000, 1000), (0, 1), "shift", "row"),      # whole sum from an unaligned base: more chunks
+    ((5, 1, 257), (0, 1, 2), "shift", "row"),    # ... two chunks where an aligned base needs one
 ]
 
 
@@ -163,9 +169,10 @@ def test_reduce_axes_validation():
     big = torch.zeros(64, 100000, device="cuda")
     d = reduce_desc(big, (1,))
     need = int(lib.pe_reduce_workspace_bytes(ctypes.byref(d)))
-    assert need == 64 * _order(big, (1,))[2] * 4
+    req = 64 * _order(big, (1,))[2] * 4           # this (aligned) source's chunk sums
+    assert need >= req                            # the query covers any base address
     out = torch.empty(64, device="cuda")
-    for ws, nb in ((None, 0), (out.data_ptr(), need - 4)):
+    for ws, nb in ((None, 0), (out.data_ptr(), req - 4)):
         rc = lib.pe_reduce_axes(ctypes.byref(d), ctypes.c_void_p(big.data_ptr()), ctypes.c_void_p(out.data_ptr()),
                                 ctypes.c_void_p(ws), nb, st)
         assert rc == -4 and "workspace" in runtime.last_error()

@@ -119,8 +119,8 @@ def test_reduce_order_choice():
     assert o == (8, 8, 1) and ws == 0
     (o, _) = _order_of(torch.zeros(64, 1026)[:, 1:], (1,))       # rows not 16-byte aligned
     assert o[:2] == (1, 64)
-    (o, ws) = _order_of(torch.zeros(64, 100000), (1,))
-    assert o[:2] == (4, 64) and o[2] > 1 and ws == 64 * o[2] * 4
+    (o, ws) = _order_of(torch.zeros(64, 100000), (1,))           # (the size covers unaligned bases too)
+    assert o[:2] == (4, 64) and o[2] > 1 and ws >= 64 * o[2] * 4
     (o, _) = _order_of(torch.zeros(5000, 100), (1,))             # 25 groups: the fewest lanes
     assert o == (4, 4, 1)
     (o, _) = _order_of(torch.zeros(5000, 20), (1,))              # short runs: a lane per output
@@ -129,3 +129,16 @@ def test_reduce_order_choice():
     assert o[:2] == (1, 1) and o[2] > 1 and ws == 64 * o[2] * 4
     (o, ws) = _order_of(torch.zeros(3, 0, 2), (1,))              # no terms
     assert ws == 0
+
+
+def test_workspace_query_covers_unaligned_sources():
+    """pe_reduce_workspace_bytes takes no source address, so its size holds
+    for a base that is not 16-byte aligned too (one-element groups, hence
+    more groups and chunks than an aligned base gets)."""
+    buf = torch.zeros(1000 * 1000 + 4)
+    h = torch.zeros(5 * 257 + 8, dtype=torch.float16)
+    for whole, shifted, axes in ((buf[:-4].reshape(1000, 1000), buf[1:-3].reshape(1000, 1000), (0, 1)),
+                                 (h[:5 * 257].reshape(5, 1, 257), h[1:1 + 5 * 257].reshape(5, 1, 257), (0, 1, 2))):
+        (oa, wa), (ou, wu) = _order_of(whole, axes), _order_of(shifted, axes)
+        assert oa[0] > 1 and ou[0] == 1 and ou[2] > oa[2]      # the unaligned plan needs more chunks
+        assert wa == wu == ou[2] * 4                            # one output: C float32 chunk sums
