@@ -80,9 +80,10 @@ def test_broadcast_multi_op_sequence(dtype, build_dir):
 def test_random_einsums_against_the_oracle(seed, build_dir):
     """150 seeded random equations per seed (tests/random_einsum.py: batch,
     free and contracted axes in random counts, sizes and orders, both dtypes,
-    a third of the operands as non-contiguous views) through the public
-    einsum against the oracle; equations with single-operand reduction axes
-    (reduce_solo_axes=True) against torch's float64 einsum."""
+    a third of the operands as non-contiguous views and some contiguous at a
+    base one element into a buffer, so not 16-byte aligned) through the
+    public einsum against the oracle; equations with single-operand reduction
+    axes (reduce_solo_axes=True) against torch's float64 einsum."""
     import random
 
     from pto_einsum import einsum
@@ -98,6 +99,10 @@ def test_random_einsums_against_the_oracle(seed, build_dir):
             ga = ga.t().contiguous().t() if ga.dim() == 2 else ga.transpose(0, -1).contiguous().transpose(0, -1)
         if gb.dim() >= 2 and rng.random() < 0.33:
             gb = gb.t().contiguous().t() if gb.dim() == 2 else gb.transpose(0, -1).contiguous().transpose(0, -1)
+        if rng.random() < 0.25:
+            flat = torch.zeros(ga.numel() + 1, dtype=dtype, device="cuda")
+            flat[1:] = ga.reshape(-1)
+            ga = flat[1:].view(ga.shape)
         what = f"random case {seed}.{i}: {eq} {s0} {s1} {dtype}{' solo' if solo else ''}"
         print(what, flush=True)
         got = einsum(eq, ga, gb, reduce_solo_axes=solo).cpu()
