@@ -158,6 +158,13 @@ bool hbm_bound(const pe_gemm_desc& d) {
 bool big_f16(const pe_gemm_desc& d, bool dl, int al, int bl) {
     if (!PE_GEMM_BIG_F16 || d.dtype != PE_F16 || !dl || d.split_k > 1) return false;
     if (gemm_big_resident(al, bl) < 1) return false;
+    // Its full-slab loads address each 16-byte vector by a 32-bit byte offset
+    // from the slab's base (256 rows, 32 k): operands whose strides reach
+    // past 2^32 bytes within a slab take the direct-load kernel (64-bit
+    // addresses) instead.
+    auto slab_span = [](int64_t rs, int64_t ks) { return (255 * rs + 31 * ks + 8) * 2; };
+    if (slab_span(d.a_ms, d.a_ks) >= (int64_t(1) << 32) || slab_span(d.b_ns, d.b_ks) >= (int64_t(1) << 32))
+        return false;
     if (d.tile == 1) return true;
     if (d.tile != 0 || d.split_k != 0 || hbm_bound(d) || d.K < 128) return false;
     const int64_t tm = ceil_div(d.M, 256), tn = ceil_div(d.N, 256);

@@ -183,6 +183,33 @@ def test_phase_skip_leaves_skipped_outputs_unwritten(eq, s0, s1):
         assert lib.pe_einsum_teardown(ctypes.c_void_p(ws)) == 0
 
 
+def test_operand_row_strides_beyond_32_bit_slab_offsets():
+    """A float16 batched GEMM whose A rows are 8.4M elements apart: a 256-row
+    slab of A spans more than 2^32 bytes, past the 32-bit per-lane load
+    offsets of the 256x256 kernel, so it must run on the 64-bit-addressed
+    direct-load kernel.  mbk,bkn->bmn with m = n = 1024, b = 2064, k = 4096
+    (17 GB per operand, 8.6 GB out); sampled outputs against float64."""
+    from pto_einsum import einsum
+
+    m, b, k, n = 1024, 2064, 4096, 1024
+    assert (255 * b * k + 31 + 8) * 2 >= 2 ** 32
+    g = torch.Generator(device="cuda").manual_seed(3)
+    A = torch.randn(m, b, k, device="cuda", dtype=torch.float16, generator=g)
+    B = torch.randn(b, k, n, device="cuda", dtype=torch.float16, generator=g)
+    print("einsum mbk,bkn->bmn", (m, b, k), (b, k, n), flush=True)
+    out = einsum("mbk,bkn->bmn", A, B)
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(0)
+    for _ in range(48):
+        bi, mi, ni = int(rng.integers(b)), int(rng.integers(m)), int(rng.integers(n))
+        a_row, b_col = A[mi, bi].double(), B[bi, :, ni].double()
+        want = float((a_row * b_col).sum())
+        bound = float((a_row.abs() * b_col.abs()).sum())
+        assert abs(float(out[bi, mi, ni]) - want) <= 2e-3 * bound, (bi, mi, ni)
+    del A, B, out
+    torch.cuda.empty_cache()
+
+
 def _gemm_direct(a, b, M, N, K, a_ms, a_ks, b_ks, b_ns, dtype_code, tile=0, split_k=0, nbatch=2):
     """C[bt] = A[bt] @ B[bt] through pe_gemm with explicit strides; A and B are
     flat device buffers holding `nbatch` operands each."""
