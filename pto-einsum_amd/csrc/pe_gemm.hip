@@ -216,6 +216,14 @@ GemmChoice choose(const pe_gemm_desc& d, bool dl = false, int al = L_MN, int bl 
     int64_t long_k_split = 0;
     c.minb = 3;
     c.nbatch_total = batch_total(d);
+    if (c.nbatch_total == 0 || d.M == 0 || d.N == 0) {
+        // An empty output: nothing is launched (the tile and split counts
+        // below would divide by its zero tiles).
+        c.bm = c.bn = 128;
+        c.nsplit = 1;
+        c.k_per_split = int(std::max<int64_t>(d.K, 1));
+        return c;
+    }
     const int bk = gemm_bk(d.dtype);
     const int64_t cus = cu_count();
     c.persist = PE_GEMM_PERSIST;
@@ -405,7 +413,7 @@ int validate_gemm(const pe_gemm_desc& d) {
 
 extern "C" int64_t pe_gemm_workspace_bytes(const pe_gemm_desc* d) {
     if (!d || pe::validate_gemm(*d) != PE_OK) return 0;
-    if (d->K == 0) return 0;
+    if (d->K == 0 || d->M == 0 || d->N == 0 || pe::batch_total(*d) == 0) return 0;
     return pe::choose(*d).ws_bytes;
 }
 

@@ -527,7 +527,7 @@ struct Plan {
 
 Plan plan(const pe_linattn_desc& d, const void* q, const void* k, const void* m) {
     Plan p{};
-    const int64_t blocks_tp = ceil_div(d.T, kTB) * ceil_div(d.P, kPB);
+    const int64_t blocks_tp = std::max<int64_t>(1, ceil_div(d.T, kTB) * ceil_div(d.P, kPB));  // (empty outputs: nothing runs)
     const int64_t sblocks = std::max<int64_t>(1, ceil_div(d.S, kSB));
     // About eight waves per CU: two blocks of four or one of eight.
     int64_t split = d.split > 0 ? d.split : ceil_div(int64_t(cu_count()) * (8 / kWaves), blocks_tp);
@@ -607,6 +607,7 @@ hipError_t pad_rows(const void* src, int64_t stride, void* dst, int64_t rows, in
 
 extern "C" int64_t pe_linear_attention_workspace_bytes(const pe_linattn_desc* d) {
     if (!d || pe::validate(*d) != PE_OK) return 0;
+    if (d->T == 0 || d->P == 0 || d->S == 0 || d->N == 0) return 0;  // nothing staged or split
     return pe::plan(*d, nullptr, nullptr, nullptr).ws_bytes;
 }
 

@@ -307,7 +307,8 @@ RedPlan plan_reduce(const pe_reduce_desc& d, const void* src) {
     for (int i = 0; i < d.nkeep; ++i) a.nout *= d.keep_shape[i];
     for (int i = 0; i < d.nred; ++i) a.nterm *= d.red_shape[i];
     const int64_t eb = d.dtype == PE_F16 ? 2 : 4;
-    if (a.nterm == 0) {
+    if (a.nterm == 0 || a.nout == 0) {
+        // No terms (every output is +0) or no outputs (nothing to do).
         p.mode = 0;
         p.V = p.L = 1;
         a.G = 0;

@@ -283,7 +283,10 @@ def parse_recipe(fn: str, shape0, shape1, device: str = "cuda") -> Dict:
             tile = _tile_size()
             mpad, npad = _pad16(L0), _pad16(L1)
             mt, ntl = min(tile, mpad), min(tile, npad)
-            if mpad % mt == 0 and npad % ntl == 0:
+            # (A zero extent pads to 0; the reference's modulo by that 0,
+            # builder.py:318-322, raises.  Such an output is empty and takes
+            # the general path.)
+            if mt > 0 and ntl > 0 and mpad % mt == 0 and npad % ntl == 0:
                 st0 = dict(zip(in0, row_major_strides(shape0)))
                 st1 = dict(zip(in1, row_major_strides(shape1)))
                 nt = dict(

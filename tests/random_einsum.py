@@ -12,11 +12,14 @@ import random
 from math import prod
 
 SIZES = [1, 2, 3, 5, 7, 8, 16, 17, 31, 32, 33, 64, 100, 128, 130, 257]
+EMPTY_SIZES = [0, 0, 1, 2, 3, 5, 17, 33, 64]  # with zero extents: empty outputs and empty sums
 LETTERS = "abcdefghijklmnopqrstuvwxyzABCDEF"
 
 
-def random_case(rng: random.Random, solo: bool = False, max_elems: float = 3e6, max_work: float = 1.5e8):
-    """(equation, shape0, shape1, has_solo_axes)."""
+def random_case(rng: random.Random, solo: bool = False, max_elems: float = 3e6, max_work: float = 1.5e8,
+                sizes=SIZES):
+    """(equation, shape0, shape1, has_solo_axes), axis extents drawn from
+    ``sizes``."""
     while True:
         nb = rng.choice([0, 0, 1, 2])
         nf0, nf1, nc = (rng.choice([0, 1, 1, 2, 3]) for _ in range(3))
@@ -36,7 +39,7 @@ def random_case(rng: random.Random, solo: bool = False, max_elems: float = 3e6, 
         rng.shuffle(in0)
         rng.shuffle(in1)
         rng.shuffle(out)
-        size = {a: rng.choice(SIZES) for a in in0 + in1}
+        size = {a: rng.choice(sizes) for a in in0 + in1}
         n0, n1, no = (prod(size[a] for a in t) for t in (in0, in1, out))
         work = no * prod(size[a] for a in con) * prod(size[a] for a in s0)
         if max(n0, n1) > max_elems or no > max_elems or work > max_work:

@@ -178,3 +178,37 @@ def test_phase_stop_define_reaches_the_plan(stop, skip, tmp_path):
     subprocess.run(cmd, check=True)
     out = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout
     assert int(out) == skip
+
+
+@pytest.mark.parametrize("eq,s0,s1", [("ij,jk->ik", (0, 5), (5, 7)), ("ij,jk->ik", (5, 5), (5, 0)),
+                                      ("bij,bjk->bik", (0, 3, 4), (0, 4, 5)), ("ij,jk->ki", (0, 4096), (4096, 16)),
+                                      ("abc,cd->adb", (0, 6, 96), (96, 80)), ("he,ew->wh", (5, 0), (0, 0))])
+def test_empty_outputs_plan_without_dividing_by_zero(eq, s0, s1):
+    """Shapes with a zero extent plan and size their workspace (host code
+    only; an integer division by the zero tile count would end the process)."""
+    b = EinsumBuilder(eq, [s0, s1], torch.float32)
+    b.parse_equation()
+    b.generate_code()
+    lib = abi.bind()
+    assert lib.pe_einsum_workspace_bytes(ctypes.byref(abi.einsum_plan(b.launch_plan))) >= 0
+    if b.launch_plan.route == 1:
+        assert lib.pe_gemm_workspace_bytes(ctypes.byref(abi.einsum_plan(b.launch_plan).gemm)) == 0
+
+
+def test_empty_reductions_and_chains_size_without_dividing_by_zero():
+    from solo_reduce_order import reduce_desc
+
+    lib = abi.bind()
+    for shape, axes in (((0, 17, 5), (2,)), ((0, 3000), (1,)), ((17, 0, 5), (2,)), ((5, 0), ())):
+        x = torch.zeros(shape)
+        d = reduce_desc(x, axes)
+        order = (ctypes.c_int64 * 3)()
+        assert lib.pe_reduce_workspace_bytes(ctypes.byref(d)) == 0
+        assert lib.pe_reduce_order(ctypes.byref(d), ctypes.c_void_p(x.data_ptr()), order) == 0
+    for T, S, N, P in ((0, 64, 16, 16), (64, 64, 16, 0), (0, 0, 16, 16), (64, 0, 16, 16), (64, 64, 0, 16)):
+        d = abi.LinAttnDesc()
+        d.qk_dtype = d.v_dtype = d.m_dtype = 0
+        d.T, d.S, d.N, d.P = T, S, N, P
+        d.q_ts, d.k_ss, d.v_ss, d.m_ts = N, N, P, S
+        d.q_numel, d.k_numel, d.v_numel, d.m_numel = max(1, T * N), max(1, S * N), max(1, S * P), max(1, T * S)
+        assert lib.pe_linear_attention_workspace_bytes(ctypes.byref(d)) == 0

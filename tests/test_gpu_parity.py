@@ -76,7 +76,7 @@ def test_broadcast_multi_op_sequence(dtype, build_dir):
         builder.cleanup()
 
 
-@pytest.mark.parametrize("seed", [1, 2])
+@pytest.mark.parametrize("seed", [1, 2, 3])
 def test_random_einsums_against_the_oracle(seed, build_dir):
     """150 seeded random equations per seed (tests/random_einsum.py: batch,
     free and contracted axes in random counts, sizes and orders, both dtypes,
@@ -87,11 +87,13 @@ def test_random_einsums_against_the_oracle(seed, build_dir):
     import random
 
     from pto_einsum import einsum
-    from random_einsum import random_case
+    from random_einsum import EMPTY_SIZES, SIZES, random_case
 
     rng = random.Random(seed)
     for i in range(150):
-        eq, s0, s1, solo = random_case(rng, solo=True, max_elems=1e6, max_work=5e7)
+        # seed 3 draws extents with zeros: empty outputs and empty sums
+        sizes = EMPTY_SIZES if seed == 3 else SIZES
+        eq, s0, s1, solo = random_case(rng, solo=True, max_elems=1e6, max_work=5e7, sizes=sizes)
         dtype = rng.choice([torch.float32, torch.float16])
         a, b = make_inputs(eq, s0, s1, dtype)
         ga, gb = a.cuda(), b.cuda()

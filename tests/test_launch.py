@@ -133,17 +133,22 @@ def test_products_take_the_stream_route(eq, s0, s1):
 
 
 def test_random_plans_compute_the_einsum():
-    """600 seeded random equations (tests/random_einsum.py), single-operand
-    reduction axes summed first as einsum(reduce_solo_axes=True) does: every
-    plan, emulated in float64, gives torch's float64 einsum."""
+    """800 seeded random equations (tests/random_einsum.py; 200 of them with
+    zero extents), single-operand reduction axes summed first as
+    einsum(reduce_solo_axes=True) does: every plan, emulated in float64, gives
+    torch's float64 einsum."""
     import random
 
     from pto_einsum import planner
     from random_einsum import random_case
 
+    from random_einsum import EMPTY_SIZES
+
     rng = random.Random(20261202)
-    for i in range(600):
-        eq, s0, s1, solo = random_case(rng, solo=True, max_elems=2e5, max_work=2e6)
+    for i in range(800):
+        # the last 200 with zero extents (empty outputs, empty sums)
+        sizes = EMPTY_SIZES if i >= 600 else None
+        eq, s0, s1, solo = random_case(rng, solo=True, max_elems=2e5, max_work=2e6, **({"sizes": sizes} if sizes else {}))
         g = np.random.default_rng(i)
         x, y = g.standard_normal(s0), g.standard_normal(s1)
         want = torch.einsum(eq, torch.from_numpy(x), torch.from_numpy(y)).numpy()
