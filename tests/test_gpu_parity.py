@@ -9,7 +9,7 @@ import pytest
 import torch
 
 import oracle
-from parity_util import RTOL, check, contraction_size, make_inputs
+from parity_util import RTOL, check, contraction_size, make_inputs, ref64_gpu
 from ref_cases import ATTENTION_CASES, BROADCAST_CASES, CHAIN_CASES, CONFIG_CASES, EINSUM_CASES
 
 pytestmark = pytest.mark.gpu
@@ -116,6 +116,66 @@ def test_random_einsums_against_the_oracle(seed, build_dir):
         else:
             want = oracle.einsum(eq, a.float().numpy(), b.float().numpy())
             check(got.numpy(), want, contraction_size(eq, s0, s1) <= 1, RTOL[dtype], what)
+
+
+def test_random_contractions_with_inf_and_nan(build_dir):
+    """60 seeded random contractions whose operands carry a sprinkle of +inf,
+    -inf and NaN: which outputs are NaN, +inf or -inf does not depend on the
+    summation order (no finite sum here comes near overflow), so the pattern
+    must equal the oracle's exactly; finite outputs meet the contraction bar."""
+    import random
+
+    from pto_einsum import einsum
+    from random_einsum import random_case
+
+    rng = random.Random(41)
+    specials = torch.tensor([float("inf"), float("-inf"), float("nan")])
+    n = 0
+    while n < 60:
+        eq, s0, s1, _ = random_case(rng, max_elems=3e5, max_work=2e7)
+        if contraction_size(eq, s0, s1) <= 1:
+            continue
+        n += 1
+        dtype = rng.choice([torch.float32, torch.float16])
+        g = torch.Generator().manual_seed(n)
+        a, b = torch.rand(s0, generator=g), torch.rand(s1, generator=g)
+        for x in (a, b):
+            flat = x.view(-1)
+            k = max(1, flat.numel() // 200)
+            flat[torch.randint(0, flat.numel(), (k,), generator=g)] = specials[torch.randint(0, 3, (k,), generator=g)]
+        a, b = a.to(dtype), b.to(dtype)
+        what = f"special case {n}: {eq} {s0} {s1} {dtype}"
+        print(what, flush=True)
+        got = einsum(eq, a.cuda(), b.cuda()).cpu().numpy()
+        want = oracle.einsum(eq, a.float().numpy(), b.float().numpy())
+        for f in (np.isnan, np.isposinf, np.isneginf):
+            assert np.array_equal(f(got), f(want)), f"{what}: {f.__name__} pattern differs"
+        fin = np.isfinite(want)
+        if fin.any():
+            scale = float(np.abs(want[fin]).max())
+            assert float(np.abs(got[fin].astype(np.float64) - want[fin]).max()) <= RTOL[dtype] * max(scale, 1e-30), what
+
+
+@pytest.mark.parametrize("dtype,tiny", [(torch.float32, 1e-41), (torch.float16, 1e-6)], ids=["f32", "f16"])
+@pytest.mark.parametrize("eq,s0,s1", [("ij,jk->ik", (64, 128), (128, 96)), ("bji,bjk->bik", (4, 77, 100), (4, 77, 150)),
+                                      ("ik,jk->ij", (512, 256), (512, 256)), ("ts,sp->tp", (256, 4096), (4096, 128)),
+                                      ("ij,jk->ik", (4096, 2048), (2048, 4096))])
+def test_subnormal_operands_are_not_flushed(eq, s0, s1, dtype, tiny, build_dir):
+    """Every A element subnormal in its own dtype, so every output is tiny:
+    a kernel that flushed subnormal inputs (or results) to zero would be off
+    by 100 % of the output scale.  Staged, direct-load, split-K and (float16
+    4096 x 2048 x 4096) 256x256 GEMMs are reached; the reference is float64
+    on the GPU, where these values are normal numbers."""
+    from pto_einsum import einsum
+
+    g = torch.Generator().manual_seed(1)
+    a = (torch.rand(s0, generator=g) * tiny).to(dtype)
+    b = torch.rand(s1, generator=g).to(dtype)
+    got = einsum(eq, a.cuda(), b.cuda()).double()
+    want = ref64_gpu(eq, a, b)
+    scale = float(want.abs().max())
+    assert scale > 0
+    assert float((got - want).abs().max()) <= RTOL[dtype] * scale, f"{eq} subnormal {dtype}"
 
 
 def test_builder_reuse(build_dir):
