@@ -124,6 +124,15 @@ struct TileArgs {
 
 constexpr int kTile = 64;
 
+// Permutation outputs from this size on are written with non-temporal
+// stores.  Lower than the GEMM / product threshold: a 67 MB gather ran 6 %
+// faster with them and a 67 MB tile transpose 3 % (cold operands), while a
+// 64 MB GEMM output or product ran 7-13 % slower; a staged einsum whose GEMM
+// reads the gathered operand right after was unchanged.
+#ifndef PE_PERMUTE_NT_MIN_BYTES
+#define PE_PERMUTE_NT_MIN_BYTES (32ll << 20)
+#endif
+
 #ifndef PE_TILE_GRID_PER_CU
 #define PE_TILE_GRID_PER_CU 32
 #endif
@@ -276,7 +285,7 @@ int run(const pe_permute_desc& d, const void* src, void* dst, hipStream_t s) {
         }
         constexpr int VEC = 16 / sizeof(W);
         constexpr int U = PE_GATHER_UNROLL;
-        a.nt = n * int64_t(sizeof(W)) >= PE_NT_MIN_BYTES;
+        a.nt = n * int64_t(sizeof(W)) >= PE_PERMUTE_NT_MIN_BYTES;
         bool vec = inner_kept && nd > 0 && inner % VEC == 0 && aligned(src, 16) && aligned(dst, 16);
         for (int k = 0; k < a.nouter && vec; ++k) vec = sst[k] % VEC == 0;
         const bool outer = a.nouter > 0;
@@ -331,7 +340,7 @@ int run(const pe_permute_desc& d, const void* src, void* dst, hipStream_t s) {
     }
     t.nbatch = nb;
     t.nbatch_total = uint32_t(nbt);
-    t.nt = n * int64_t(sizeof(W)) >= PE_NT_MIN_BYTES;
+    t.nt = n * int64_t(sizeof(W)) >= PE_PERMUTE_NT_MIN_BYTES;
     constexpr int VEC = 16 / sizeof(W);
     bool vload = aligned(src, 16) && t.src_q_stride % VEC == 0;
     bool vstore = aligned(dst, 16) && t.dst_p_stride % VEC == 0;
