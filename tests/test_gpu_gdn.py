@@ -201,3 +201,39 @@ def test_linear_attention_graph():
         got = graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(got, eager), f"replay {rep} differs"
+
+
+def test_random_einsum_sequences_replay_bit_identical():
+    """30 seeded random sequences of two to five einsums (tests/random_einsum.py:
+    product, direct, staged and split-K GEMM routes, single-operand reduction
+    axes, both dtypes) captured by StageGraph and replayed three times with
+    new inputs written in place: every output of every replay equals an
+    eager call on the same inputs bit for bit."""
+    import random
+
+    from pto_einsum import StageGraph, einsum
+    from random_einsum import random_case
+
+    rng = random.Random(5)
+    for it in range(30):
+        cases = []
+        for _ in range(rng.choice([2, 3, 5])):
+            eq, s0, s1, solo = random_case(rng, solo=True, max_elems=3e5, max_work=2e7)
+            cases.append((eq, s0, s1, solo, rng.choice([torch.float32, torch.float16])))
+        print(f"graph sequence {it}: " + "; ".join(c[0] for c in cases), flush=True)
+        ins = [(torch.rand(c[1], device="cuda").to(c[4]), torch.rand(c[2], device="cuda").to(c[4])) for c in cases]
+
+        def fn():
+            return [einsum(c[0], a, b, reduce_solo_axes=c[3]) for c, (a, b) in zip(cases, ins)]
+
+        graph = StageGraph(fn)
+        for rep in range(3):
+            for a, b in ins:
+                a.copy_(torch.rand(a.shape, device="cuda").to(a.dtype))
+                b.copy_(torch.rand(b.shape, device="cuda").to(b.dtype))
+            graph.replay()
+            torch.cuda.synchronize()
+            eager = fn()
+            torch.cuda.synchronize()
+            for k, (got, want) in enumerate(zip(graph.outputs, eager)):
+                assert torch.equal(got, want), f"sequence {it} replay {rep} output {k}"
