@@ -178,6 +178,19 @@ def test_subnormal_operands_are_not_flushed(eq, s0, s1, dtype, tiny, build_dir):
     assert float((got - want).abs().max()) <= RTOL[dtype] * scale, f"{eq} subnormal {dtype}"
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16], ids=["f32", "f16"])
+def test_batched_partial_output_tiles(dtype, build_dir):
+    """tests/test_einsum.py:161-178: the reference's case for batched (I > 1)
+    partial output tiles, which it skips (and rejects, :193-197) until that
+    path lands; here it runs, against the oracle."""
+    from pto_einsum import einsum
+
+    eq, s0, s1 = "bij,bjk->bik", (4, 200, 64), (4, 64, 128)
+    a, b = make_inputs(eq, s0, s1, dtype)
+    got = einsum("bij, bjk -> bik", a.cuda(), b.cuda()).cpu().numpy()
+    check(got, oracle.einsum(eq, a.float().numpy(), b.float().numpy()), False, RTOL[dtype], eq)
+
+
 def test_builder_reuse(build_dir):
     """test_einsum.py:208-241: a runner reused with fresh data, incl. K != C."""
     from pto_einsum import EinsumBuilder
