@@ -35,6 +35,12 @@
 #define PE_GEMM_BIG_MIN_FILL 0.95
 #endif
 
+// float32 GEMMs that would split a K of at most this length over blocks run
+// the k-split kernel (pe_gemm_ks.h) instead: one launch, no partials.
+#ifndef PE_GEMM_KS_MAX_K
+#define PE_GEMM_KS_MAX_K 1024
+#endif
+
 // float16 GEMMs bound by matrix-core issue take 256x256 tiles (pe_gemm_big.h)
 // when those fill at least one round of CUs.
 #ifndef PE_GEMM_BIG_F16
@@ -489,6 +495,36 @@ extern "C" int pe_gemm(const pe_gemm_desc* d, const void* a, const void* b, floa
         if (!ws || ws_bytes < ch.ws_bytes) return fail(PE_ERR_WORKSPACE, "gemm: split-K workspace missing or too small");
         if (nb * d->M * d->N >= (int64_t(1) << 32))
             return fail(PE_ERR_UNSUPPORTED, "gemm: split-K output too large");
+    }
+    if (ch.nsplit > 1 && d->dtype == PE_F32 && dl && d->split_k == 0 && d->tile == 0 &&
+        d->K <= PE_GEMM_KS_MAX_K && gemm_ks_resident(al, bl) >= 1) {
+        // A short K that the tile choice would split: the k-split kernel,
+        // one block per 32x32 tile (at most 16x the split grid's 64x64 or
+        // 128x128 tiles, fewer than 2^31 blocks).
+        GemmArgs g{};
+        g.a = a; g.b = b; g.c = c;
+        g.partial = nullptr;
+        g.M = int32_t(d->M); g.N = int32_t(d->N); g.K = int32_t(d->K);
+        g.nsplit = 1;
+        g.k_per_split = int32_t(d->K);
+        g.tiles_m = int32_t(ceil_div(d->M, kKsTile));
+        g.tiles_n = int32_t(ceil_div(d->N, kKsTile));
+        g.tiles_per_batch = uint32_t(g.tiles_m) * uint32_t(g.tiles_n);
+        g.nbatch_total = uint32_t(nb);
+        g.total_blocks = g.tiles_per_batch * g.nbatch_total;
+        g.grid = g.total_blocks;
+        g.store_nt = nb * d->M * d->N * 4 >= PE_NT_MIN_BYTES;
+        g.a_ms = d->a_ms; g.a_ks = d->a_ks; g.b_ks = d->b_ks; g.b_ns = d->b_ns;
+        g.c_ms = d->c_ms; g.c_ns = d->c_ns;
+        g.nbatch = d->nbatch;
+        for (int i = 0; i < d->nbatch; ++i) {
+            g.batch_div[i].init(uint32_t(d->batch_shape[i]));
+            g.a_bs[i] = d->a_bstride[i];
+            g.b_bs[i] = d->b_bstride[i];
+            g.c_bs[i] = d->c_bstride[i];
+        }
+        PE_CHECK_HIP(launch_gemm_ks(al, bl, g, s));
+        return PE_OK;
     }
     GemmArgs g{};
     g.a = a; g.b = b; g.c = c;

@@ -164,7 +164,6 @@ struct DlOperand {
     static constexpr int ELEMS = ROWS * BK;           // elements per stage
     static constexpr int NCHUNK = ELEMS * E::kBytes / 1024;  // 1 KB chunks, one wave instruction each
     static constexpr int NI = NCHUNK / 4;             // instructions per wave per slab
-    static_assert(NI >= 1 && NCHUNK % 4 == 0, "every wave issues whole chunks");
     static constexpr int LPR = ROWS / EPV;            // L_MN: lanes (vectors) per k row
     static constexpr int KPC = 64 / LPR;              // L_MN: k rows per chunk
     static_assert(kF32 || LAYOUT == L_K || LPR >= 8, "float16 k-major swizzle needs 8 vectors per row");
@@ -187,21 +186,33 @@ struct DlOperand {
     // row 0, slab k 0); rows_left / k_left: valid extent from there.
     __device__ __forceinline__ static void load(const T* base, int64_t rs, int64_t ks, int rows_left,
                                                 int k_left, T* stage, int lane, int wave) {
+        static_assert(NI >= 1 && NCHUNK % 4 == 0, "every wave issues whole chunks");
 #pragma unroll
-        for (int i = 0; i < NI; ++i) {
-            const int c = i * 4 + wave;
-            int r, k;
-            if constexpr (LAYOUT == L_MN) {
-                const int kk = c * KPC + lane / LPR;
-                k = min(kk, k_left - 1);
-                r = min(((lane % LPR) ^ kswz(kk)) * EPV, rows_left - EPV);
-            } else {
-                r = min(c * 16 + lane / 4, rows_left - 1);
-                k = min(EPV * ((lane % 4) ^ (lane / 16)), k_left - EPV);
-            }
-            dma16(reinterpret_cast<const float*>(base + int64_t(r) * rs + int64_t(k) * ks),
-                  reinterpret_cast<const float*>(stage + c * (1024 / E::kBytes)));
+        for (int i = 0; i < NI; ++i) load_chunk(base, rs, ks, rows_left, k_left, stage, lane, i * 4 + wave);
+    }
+
+    // Row and k (relative to the stage's first row and k) that lane `lane`
+    // fetches for chunk c (0 <= c < NCHUNK) of a stage, clamped into the
+    // valid extent.  Needs rows_left >= EPV (L_MN) and k_left >= EPV (L_K)
+    // or >= 1 (L_MN).
+    __device__ __forceinline__ static void chunk_rk(int lane, int c, int rows_left, int k_left, int& r, int& k) {
+        if constexpr (LAYOUT == L_MN) {
+            const int kk = c * KPC + lane / LPR;
+            k = min(kk, k_left - 1);
+            r = min(((lane % LPR) ^ kswz(kk)) * EPV, rows_left - EPV);
+        } else {
+            r = min(c * 16 + lane / 4, rows_left - 1);
+            k = min(EPV * ((lane % 4) ^ (lane / 16)), k_left - EPV);
         }
+    }
+
+    // One wave's load of chunk c of a stage.
+    __device__ __forceinline__ static void load_chunk(const T* base, int64_t rs, int64_t ks, int rows_left,
+                                                      int k_left, T* stage, int lane, int c) {
+        int r, k;
+        chunk_rk(lane, c, rows_left, k_left, r, k);
+        dma16(reinterpret_cast<const float*>(base + int64_t(r) * rs + int64_t(k) * ks),
+              reinterpret_cast<const float*>(stage + c * (1024 / E::kBytes)));
     }
 
     // Zeroes every k >= k_left of a stage (0 < k_left < BK).
