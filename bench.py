@@ -24,7 +24,9 @@ events: the figure is the GPU time per einsum.
 
 ``large_f16`` times 8192^3 float16 contractions (float32 output) in the
 NN and NT layouts on the dense float16 MFMA roof, with torch.matmul (the
-vendor library, float16 output) beside them.
+vendor library, float16 output) beside them; ``vendor_thin`` times
+torch.matmul on config 5's two thin contractions (5.1, 5.3) with the same
+operand rotation as the ``per_config`` rows.
 
 ``gdn`` times the GDN contraction set at the reference's sizes the same way,
 and ``gdn_stages`` two of its stage sequences issued eagerly (one Python call
@@ -713,6 +715,47 @@ def time_torch_matmul(dev):
     return out
 
 
+def time_torch_thin(dev, calls=50):
+    """torch.matmul (hipBLASLt) on config 5's two thin contractions, with the
+    operand rotation of the per-config rows: 5.1 tn,sn->ts in float16 (float16
+    output, half the bytes this path's float32 output writes) and 5.3
+    ts,sp->tp in float32 with TF32 off (this path's precision)."""
+    import torch
+
+    g = torch.Generator().manual_seed(51)
+    f16 = torch.float16
+    cases = (("5.1", "tn,sn->ts", (torch.randn(4096, 128, generator=g) * 128 ** -0.5).to(f16),
+              (torch.randn(4096, 128, generator=g) * 128 ** -0.5).to(f16), lambda a, b: torch.matmul(a, b.t()),
+              4096 * 4096 * 2),
+             ("5.3", "ts,sp->tp", torch.rand(4096, 4096, generator=g), torch.randn(4096, 128, generator=g),
+              torch.matmul, 4096 * 128 * 4))
+    tf32 = torch.backends.cuda.matmul.allow_tf32
+    torch.backends.cuda.matmul.allow_tf32 = False
+    out = []
+    try:
+        for cfg, eq, a, b, fn, out_bytes in cases:
+            a, b = a.to(dev), b.to(dev)
+            sets = replicate((a, b), n_sets(a.nbytes + b.nbytes + out_bytes))
+            for i in range(3):
+                fn(*sets[i % len(sets)])
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for i in range(calls):
+                fn(*sets[i % len(sets)])
+            e1.record()
+            torch.cuda.synchronize()
+            t = e0.elapsed_time(e1) / calls
+            out.append(dict(config=cfg, equation=f"torch.matmul {eq} ({a.dtype} in and out)", us=round(t * 1e3, 2),
+                            operand_sets=len(sets)))
+            log(f"bench: torch.matmul {cfg} {eq} {t * 1e3:.1f} us")
+            del sets, a, b
+    finally:
+        torch.backends.cuda.matmul.allow_tf32 = tf32
+    torch.cuda.empty_cache()
+    return out
+
+
 # ------------------------------------------------------------ CPU baseline --
 
 def cpu_baseline(budget_s=10.0):
@@ -813,6 +856,7 @@ def main():
             if c["config"].startswith("5.F"):
                 c["three_einsums_us"] = round(chain, 2)
         rows["large_f16"] += time_torch_matmul(dev)
+        rows["vendor_thin"] = time_torch_thin(dev)
         rows["gdn_stages"] = time_gdn_stages(dev, args.steps)
 
     cpu = None
