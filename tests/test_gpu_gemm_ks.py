@@ -121,3 +121,33 @@ def test_k_split_gemm_special_values():
     assert torch.equal(torch.isinf(got), torch.isinf(want))
     fin = torch.isfinite(want)
     assert torch.allclose(got.double()[fin], want[fin], rtol=1e-4, atol=1e-3)
+
+
+EINSUMS = [
+    # equation, sizes (i, j = contracted, k, b); float32 GEMMs whose tile choice splits a K <= 1024
+    ("ij,jk->ik", dict(i=256, j=256, k=256)),        # config 1
+    ("ij,jk->ki", dict(i=200, j=300, k=120)),        # transposed output store
+    ("ji,kj->ik", dict(i=96, j=1000, k=64)),         # both operands read transposed
+    ("bij,bjk->bki", dict(b=3, i=64, j=500, k=96)),  # batched, permuted output
+    ("ijx,jxk->ik", dict(i=128, j=16, x=40, k=128)), # two contracted axes merged into K = 640
+]
+
+
+@pytest.mark.parametrize("eq,sizes", EINSUMS, ids=[e for e, _ in EINSUMS])
+def test_k_split_gemm_through_einsum(eq, sizes):
+    """The k-split kernel behind the public einsum (layouts, batches and
+    permuted stores chosen by the planner), against float64."""
+    from pto_einsum import einsum
+
+    t0, rest = eq.split(",")
+    t1 = rest.split("->")[0]
+    g = torch.Generator().manual_seed(len(eq) + sum(sizes.values()))
+    a = torch.randn(*[sizes[c] for c in t0], generator=g)
+    b = torch.randn(*[sizes[c] for c in t1], generator=g)
+    got = einsum(eq, a.cuda(), b.cuda()).cpu()
+    want = torch.einsum(eq, a.double(), b.double())
+    bound = torch.einsum(eq, a.double().abs(), b.double().abs())
+    assert got.shape == want.shape
+    err = (got.double() - want).abs()
+    assert bool((err <= 1e-5 * bound + 1e-6).all()), float((err - 1e-5 * bound).max())
+    assert torch.equal(got, einsum(eq, a.cuda(), b.cuda()).cpu())
