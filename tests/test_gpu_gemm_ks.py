@@ -1,6 +1,7 @@
-"""The k-split float32 GEMM (pe_gemm_ks.h): float32 products whose tile choice
-splits a K of at most 1024 over blocks run as one block per 32x32 output tile,
-the block's four waves splitting K, with no workspace traffic.  Every operand
+"""The k-split float32 GEMM (pe_gemm_ks.h): float32 products with a K of at
+most 1024 whose tile choice splits K over blocks, or leaves at most one 64x64
+tile per CU, run as one block per 32x32 or 64x64 output tile, the block's four
+waves splitting K, with no workspace traffic.  Every operand
 layout pairing (rows or k contiguous), batches, partial tiles, K tails that
 end inside a stage's first, middle or last sub-slab, and transposed output
 strides, against a float64 reference with a bound of 1e-5 sum |a||b| (float32
@@ -79,7 +80,28 @@ def test_k_split_gemm_against_float64(M, N, K, nb, al, bl):
     assert torch.equal(outs[0], outs[1])
 
 
-@pytest.mark.parametrize("M,N,K,nb", [(100, 68, 300, 2), (256, 256, 256, 1)])
+ONE_PER_CU = [
+    # M, N, K, batch: 64x64 tiles give each CU at most one (unsplit grids; 64x64 k-split tiles
+    # where they give each CU three quarters of one or more)
+    (1024, 1024, 512, 1),    # 256 tiles of 64x64
+    (1000, 1000, 300, 1),    # partial tiles, K tail
+    (960, 1024, 1000, 1),    # 240 tiles, K tail in the last stage's last sub-slab
+    (512, 512, 768, 4),      # batched: 4 x 64 tiles
+    (640, 640, 256, 1),      # 100 tiles: 32x32 k-split tiles
+]
+
+
+@pytest.mark.parametrize("al,bl", [("mn", "mn"), ("mn", "k"), ("k", "mn"), ("k", "k")])
+@pytest.mark.parametrize("M,N,K,nb", ONE_PER_CU)
+def test_k_split_gemm_one_tile_per_cu(M, N, K, nb, al, bl):
+    outs, want, bound, _ = _run(M, N, K, nb, al, bl, "rows", M + 3 * N + K + nb)
+    err = (outs[0].double() - want).abs()
+    assert not torch.isnan(outs[0]).any()
+    assert bool((err <= 1e-5 * bound + 1e-6).all()), float((err - 1e-5 * bound).max())
+    assert torch.equal(outs[0], outs[1])
+
+
+@pytest.mark.parametrize("M,N,K,nb", [(100, 68, 300, 2), (256, 256, 256, 1), (1000, 1000, 300, 1)])
 def test_k_split_gemm_transposed_output(M, N, K, nb):
     outs, want, bound, _ = _run(M, N, K, nb, "mn", "mn", "cols", 5 + M)
     err = (outs[0].double() - want).abs()
