@@ -4,8 +4,10 @@
 // Grids with fewer 128 x 128 tiles than CUs split K over blocks, and a
 // second kernel sums the split partials in order (pe_gemm.hip).  Where K is
 // short (<= 1024) that costs a second launch and a round trip of the
-// partials for a few microseconds of MFMA work.  Here the tiles are 32 x 32,
-// enough for every CU, and each block walks all of K itself: a stage holds
+// partials for a few microseconds of MFMA work; unsplit grids of one 64 x 64
+// tile per CU leave one wave per SIMD walking all of K.  Here the tiles are
+// 32 x 32 (or 64 x 64 where those still give each CU about one), and each
+// block's four waves walk K together: a stage holds
 // 4 x SPW sub-slabs, each laid out exactly as a direct-load kernel's slab
 // (pe_gemm_dl.h: 64 bytes of k per row, the same swizzles and fragment
 // reads); wave w accumulates the whole tile over sub-slabs q * 4 + w of every
