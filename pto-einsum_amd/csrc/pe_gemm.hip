@@ -36,7 +36,7 @@
 #endif
 
 // float32 GEMMs with a K of at most this length whose tile choice splits K
-// over blocks, or leaves at most one 64x64 tile per CU, run the k-split
+// over blocks, or leaves at most two 64x64 tiles per CU, run the k-split
 // kernel (pe_gemm_ks.h) instead: one launch, no partials, four waves per
 // tile walking K together.
 #ifndef PE_GEMM_KS_MAX_K
@@ -499,19 +499,21 @@ extern "C" int pe_gemm(const pe_gemm_desc* d, const void* a, const void* b, floa
             return fail(PE_ERR_UNSUPPORTED, "gemm: split-K output too large");
     }
     // A short K that the tile choice would split, or (K >= 256) whose 64x64
-    // tiles give each CU at most one: the k-split kernel, one block per 64x64
+    // tiles give each CU at most two: the k-split kernel, one block per 64x64
     // tile where those give each CU between three quarters of one and one,
     // else per 32x32 tile (at most 16x the split grid's 64x64 or 128x128
     // tiles, fewer than 2^31 blocks).  Measured on one MI355X against the
     // split or unsplit grid: 256^3 7.4 -> 4.9 us, 512^2 x 1024 15.5 -> 10.8,
-    // 1024^3 36.2 -> 25.5, 1024^2 x 512 19.5 -> 15.9, 1024^2 x 256 11.3 ->
-    // 10.8; 2048^2 x 256 (four 64x64 tiles per CU) stays at 25.9 against
-    // 32.3, and 64x64 k-split tiles lost where they left CUs idle (768^2 x
+    // 1024^3 36.2 -> 25.5, 1024^2 x 512 19.5 -> 15.9, 1024 x 1536 x 1024
+    // 51.2 -> 36.2, 1280^2 x 768 39.4 -> 33.4, 2048 x 1024 x 512 28.4 ->
+    // 27.4; more 64x64 tiles per CU stay on them (2048 x 1536 x 256, three
+    // per CU: 21.6 against 25.3; 1536^2 x 1024, 2.25 per CU: 52.2 against
+    // 53.3), and 64x64 k-split tiles lost where they left CUs idle (768^2 x
     // 1024: 24.6 against 19.2 us on 32x32 ones).
     const int64_t cus = cu_count();
     const int64_t tiles64 = nb * ceil_div(d->M, 64) * ceil_div(d->N, 64);
     const int ks_tile = (4 * tiles64 >= 3 * cus && tiles64 <= cus) ? 64 : 32;
-    if ((ch.nsplit > 1 || (tiles64 <= cus && d->K >= 256)) && d->dtype == PE_F32 && dl && d->split_k == 0 &&
+    if ((ch.nsplit > 1 || (tiles64 <= 2 * cus && d->K >= 256)) && d->dtype == PE_F32 && dl && d->split_k == 0 &&
         d->tile == 0 && d->K <= PE_GEMM_KS_MAX_K && gemm_ks_resident(al, bl, ks_tile) >= 1) {
         GemmArgs g{};
         g.a = a; g.b = b; g.c = c;
