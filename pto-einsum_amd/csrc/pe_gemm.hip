@@ -510,11 +510,17 @@ extern "C" int pe_gemm(const pe_gemm_desc* d, const void* a, const void* b, floa
     // per CU: 21.6 against 25.3; 1536^2 x 1024, 2.25 per CU: 52.2 against
     // 53.3), and 64x64 k-split tiles lost where they left CUs idle (768^2 x
     // 1024: 24.6 against 19.2 us on 32x32 ones).
+    // Split grids with K up to twice that length take it too when its 32x32
+    // tiles give every CU one (1024 x 1536 x 2048 83.9 -> 66.9 us, 1536^2 x
+    // 2048 113.7 -> 98.8, 512^2 x 2048 23.0 -> 18.8; 2048 x 1024 x 2048 84.6
+    // against 88.1; fewer tiles lost: 1024 x 128 x 2048 16.9 against 18.7).
     const int64_t cus = cu_count();
     const int64_t tiles64 = nb * ceil_div(d->M, 64) * ceil_div(d->N, 64);
+    const int64_t tiles32 = nb * ceil_div(d->M, 32) * ceil_div(d->N, 32);
     const int ks_tile = (4 * tiles64 >= 3 * cus && tiles64 <= cus) ? 64 : 32;
-    if ((ch.nsplit > 1 || (tiles64 <= 2 * cus && d->K >= 256)) && d->dtype == PE_F32 && dl && d->split_k == 0 &&
-        d->tile == 0 && d->K <= PE_GEMM_KS_MAX_K && gemm_ks_resident(al, bl, ks_tile) >= 1) {
+    const bool ks_k = d->K <= PE_GEMM_KS_MAX_K ? (ch.nsplit > 1 || (tiles64 <= 2 * cus && d->K >= 256))
+                                               : (d->K <= 2 * PE_GEMM_KS_MAX_K && ch.nsplit > 1 && tiles32 >= cus);
+    if (ks_k && d->dtype == PE_F32 && dl && d->split_k == 0 && d->tile == 0 && gemm_ks_resident(al, bl, ks_tile) >= 1) {
         GemmArgs g{};
         g.a = a; g.b = b; g.c = c;
         g.partial = nullptr;

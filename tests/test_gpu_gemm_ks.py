@@ -1,11 +1,12 @@
 """The k-split float32 GEMM (pe_gemm_ks.h): float32 products with a K of at
-most 1024 whose tile choice splits K over blocks, or leaves at most one 64x64
-tile per CU, run as one block per 32x32 or 64x64 output tile, the block's four
+most 1024 whose tile choice splits K over blocks, or leaves at most two 64x64
+tiles per CU, and split ones with a K of at most 2048 whose 32x32 tiles give
+every CU one, run as one block per 32x32 or 64x64 output tile, the block's four
 waves splitting K, with no workspace traffic.  Every operand
 layout pairing (rows or k contiguous), batches, partial tiles, K tails that
 end inside a stage's first, middle or last sub-slab, and transposed output
 strides, against a float64 reference with a bound of 1e-5 sum |a||b| (float32
-sums of at most 1024 terms); repeated calls are bit-identical."""
+sums of at most 2048 terms); repeated calls are bit-identical."""
 import ctypes
 
 import pytest
@@ -88,6 +89,8 @@ ONE_PER_CU = [
     (960, 1024, 1000, 1),    # 240 tiles, K tail in the last stage's last sub-slab
     (512, 512, 768, 4),      # batched: 4 x 64 tiles
     (640, 640, 256, 1),      # 100 tiles: 32x32 k-split tiles
+    (768, 768, 2048, 1),     # split grid with K = 2048 and 576 tiles of 32x32
+    (512, 512, 1988, 2),     # the same with a K tail
 ]
 
 
