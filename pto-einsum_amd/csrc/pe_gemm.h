@@ -115,13 +115,13 @@ hipError_t launch_gemm_dl(int dtype, int bm, int bn, int minb, int al, int bl, b
                           hipStream_t s);
 hipError_t launch_gemm_f16(int bm, int bn, int alayout, int blayout, int persist, const GemmArgs& g,
                            hipStream_t s);
-// k-split float32 kernel (pe_gemm_ks.h): 32x32 or 64x64 tiles (`tile`), one
-// block per tile and batch, the block's waves splitting K; L_MN or L_K
-// operands under the gemm_dl_eligible conditions, no workspace.
-// gemm_ks_resident: resident blocks per CU (0 when it spilled or for other
-// layouts and tiles).
-int gemm_ks_resident(int alayout, int blayout, int tile);
-hipError_t launch_gemm_ks(int alayout, int blayout, int tile, const GemmArgs& g, hipStream_t s);
+// k-split kernel (pe_gemm_ks.h): float32 32x32 or 64x64 tiles, float16 64x64
+// tiles (`tile`), one block per tile and batch, the block's waves splitting
+// K; L_MN or L_K operands under the gemm_dl_eligible conditions, no
+// workspace.  gemm_ks_resident: resident blocks per CU (0 when it spilled or
+// for other dtypes, layouts and tiles).
+int gemm_ks_resident(int dtype, int alayout, int blayout, int tile);
+hipError_t launch_gemm_ks(int dtype, int alayout, int blayout, int tile, const GemmArgs& g, hipStream_t s);
 // Large float16 kernel (pe_gemm_big.h): 256x256 tiles, one block per CU,
 // operands L_MN or L_K under the gemm_dl_eligible conditions, no K split.
 // gemm_big_resident: resident blocks per CU (0 when it spilled).

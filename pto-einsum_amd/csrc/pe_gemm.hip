@@ -514,13 +514,26 @@ extern "C" int pe_gemm(const pe_gemm_desc* d, const void* a, const void* b, floa
     // tiles give every CU one (1024 x 1536 x 2048 83.9 -> 66.9 us, 1536^2 x
     // 2048 113.7 -> 98.8, 512^2 x 2048 23.0 -> 18.8; 2048 x 1024 x 2048 84.6
     // against 88.1; fewer tiles lost: 1024 x 128 x 2048 16.9 against 18.7).
+    // float16 split grids take its 64x64 tiles (float16 MFMAs are 16x the
+    // float32 rate, so the split's partial round trip weighs more) when those
+    // give every CU one (K <= 8192) or a quarter of the CUs one (K <= 2048):
+    // 1024^3 19.9 -> 9.8 us, 768^2 x 2048 21.7 -> 12.6, 1024^2 x 8192 44.8 ->
+    // 37.6, 512^2 x 1024 12.7 -> 8.7; fewer tiles or longer K lost (256^2 x
+    // 2048 9.6 against 12.1, 4096 x 128 x 4096 22.6 against 26.4).
     const int64_t cus = cu_count();
     const int64_t tiles64 = nb * ceil_div(d->M, 64) * ceil_div(d->N, 64);
     const int64_t tiles32 = nb * ceil_div(d->M, 32) * ceil_div(d->N, 32);
-    const int ks_tile = (4 * tiles64 >= 3 * cus && tiles64 <= cus) ? 64 : 32;
-    const bool ks_k = d->K <= PE_GEMM_KS_MAX_K ? (ch.nsplit > 1 || (tiles64 <= 2 * cus && d->K >= 256))
-                                               : (d->K <= 2 * PE_GEMM_KS_MAX_K && ch.nsplit > 1 && tiles32 >= cus);
-    if (ks_k && d->dtype == PE_F32 && dl && d->split_k == 0 && d->tile == 0 && gemm_ks_resident(al, bl, ks_tile) >= 1) {
+    int ks_tile = (4 * tiles64 >= 3 * cus && tiles64 <= cus) ? 64 : 32;
+    bool ks_k;
+    if (d->dtype == PE_F32) {
+        ks_k = d->K <= PE_GEMM_KS_MAX_K ? (ch.nsplit > 1 || (tiles64 <= 2 * cus && d->K >= 256))
+                                        : (d->K <= 2 * PE_GEMM_KS_MAX_K && ch.nsplit > 1 && tiles32 >= cus);
+    } else {
+        ks_tile = 64;
+        ks_k = ch.nsplit > 1 && ((tiles64 >= cus && d->K <= 8 * PE_GEMM_KS_MAX_K) ||
+                                 (4 * tiles64 >= cus && d->K <= 2 * PE_GEMM_KS_MAX_K));
+    }
+    if (ks_k && dl && d->split_k == 0 && d->tile == 0 && gemm_ks_resident(d->dtype, al, bl, ks_tile) >= 1) {
         GemmArgs g{};
         g.a = a; g.b = b; g.c = c;
         g.partial = nullptr;
@@ -543,7 +556,7 @@ extern "C" int pe_gemm(const pe_gemm_desc* d, const void* a, const void* b, floa
             g.b_bs[i] = d->b_bstride[i];
             g.c_bs[i] = d->c_bstride[i];
         }
-        PE_CHECK_HIP(launch_gemm_ks(al, bl, ks_tile, g, s));
+        PE_CHECK_HIP(launch_gemm_ks(d->dtype, al, bl, ks_tile, g, s));
         return PE_OK;
     }
     GemmArgs g{};

@@ -1,8 +1,9 @@
-"""The k-split float32 GEMM (pe_gemm_ks.h): float32 products with a K of at
-most 1024 whose tile choice splits K over blocks, or leaves at most two 64x64
-tiles per CU, and split ones with a K of at most 2048 whose 32x32 tiles give
-every CU one, run as one block per 32x32 or 64x64 output tile, the block's four
-waves splitting K, with no workspace traffic.  Every operand
+"""The k-split GEMM (pe_gemm_ks.h): float32 products with a K of at most
+1024 whose tile choice splits K over blocks, or leaves at most two 64x64 tiles
+per CU, and split ones with a K of at most 2048 whose 32x32 tiles give every
+CU one, and float16 split grids whose 64x64 tiles give every CU (K <= 8192) or
+a quarter of the CUs (K <= 2048) one, run as one block per 32x32 or 64x64
+output tile, the block's four waves splitting K, with no workspace traffic.  Every operand
 layout pairing (rows or k contiguous), batches, partial tiles, K tails that
 end inside a stage's first, middle or last sub-slab, and transposed output
 strides, against a float64 reference with a bound of 1e-5 sum |a||b| (float32
@@ -25,10 +26,10 @@ def _stream():
     return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
 
-def _run(M, N, K, nb, al, bl, ct, seed):
+def _run(M, N, K, nb, al, bl, ct, seed, dtype=torch.float32):
     g = torch.Generator().manual_seed(seed)
-    A = torch.randn(nb, M, K, generator=g)
-    B = torch.randn(nb, K, N, generator=g)
+    A = torch.randn(nb, M, K, generator=g).to(dtype)
+    B = torch.randn(nb, K, N, generator=g).to(dtype)
     # A: "mn" stored [b][K][M] (m contiguous), "k" stored [b][M][K]
     if al == "mn":
         a_buf, a_ms, a_ks = A.transpose(1, 2).contiguous(), 1, M
@@ -40,7 +41,8 @@ def _run(M, N, K, nb, al, bl, ct, seed):
     else:
         b_buf, b_ks, b_ns = B.transpose(1, 2).contiguous(), 1, K
     c_ms, c_ns = (N, 1) if ct == "rows" else (1, M)
-    d = launch.GemmDesc(dtype=launch.DT_F32, batch_shape=[nb], a_bstride=[M * K], b_bstride=[K * N],
+    code = launch.DT_F32 if dtype == torch.float32 else launch.DT_F16
+    d = launch.GemmDesc(dtype=code, batch_shape=[nb], a_bstride=[M * K], b_bstride=[K * N],
                         c_bstride=[M * N], M=M, N=N, K=K, a_ms=a_ms, a_ks=a_ks, b_ks=b_ks, b_ns=b_ns,
                         c_ms=c_ms, c_ns=c_ns, a_numel=nb * M * K, b_numel=nb * K * N, c_numel=nb * M * N)
     cd = abi.gemm_desc(d)
@@ -101,6 +103,28 @@ def test_k_split_gemm_one_tile_per_cu(M, N, K, nb, al, bl):
     err = (outs[0].double() - want).abs()
     assert not torch.isnan(outs[0]).any()
     assert bool((err <= 1e-5 * bound + 1e-6).all()), float((err - 1e-5 * bound).max())
+    assert torch.equal(outs[0], outs[1])
+
+
+F16_CASES = [
+    # M, N, K, batch: float16 split grids whose 64x64 tiles give every CU one, or a quarter of the CUs one
+    (1024, 1024, 1024, 1),
+    (768, 768, 2048, 1),
+    (512, 512, 1000, 2),     # K tail
+    (200, 520, 776, 3),      # partial tiles, batched
+    (1024, 1024, 8192, 1),   # the longest K this route takes
+]
+
+
+@pytest.mark.parametrize("al,bl", [("mn", "mn"), ("mn", "k"), ("k", "mn"), ("k", "k")])
+@pytest.mark.parametrize("M,N,K,nb", F16_CASES)
+def test_k_split_gemm_float16(M, N, K, nb, al, bl):
+    outs, want, bound, ws_bytes = _run(M, N, K, nb, al, bl, "rows", 7 * M + N + K, torch.float16)
+    assert ws_bytes > 0  # a split grid: the k-split kernel takes the call
+    err = (outs[0].double() - want).abs()
+    tol = 1e-5 if K <= 2048 else 4e-5   # float32 sums of K / 4 exact float16 products per wave
+    assert not torch.isnan(outs[0]).any()
+    assert bool((err <= tol * bound + 1e-6).all()), float((err - tol * bound).max())
     assert torch.equal(outs[0], outs[1])
 
 
