@@ -25,10 +25,11 @@
 // LDS afterwards, as in the direct-load kernel.  Every wave issues the same
 // number of loads per stage and loads complete in issue order, so s_waitcnt
 // vmcnt(ahead x loads per stage) waits for exactly the stage about to be read.
-// Measured on MI355X (float32): faster than the split-K path up to K = 1024
+// Measured on MI355X: float32 faster than the split-K path up to K = 1024
 // (256^3 7.4 -> 4.9 us, 512^2 x 1024 15.5 -> 10.8), no faster beyond (512^2 x
-// 4096 34.6 against 34.5, 1024 x 128 x 2048 16.9 against 18.7); the grids it
-// takes are chosen in pe_gemm.hip.
+// 4096 34.6 against 34.5, 1024 x 128 x 2048 16.9 against 18.7); float16 64 x
+// 64 tiles faster up to K = 8192 where they fill the CUs (1024^3 19.9 -> 9.6
+// us); the grids it takes are chosen in pe_gemm.hip.
 #pragma once
 
 #include "pe_gemm_dl.h"
