@@ -261,13 +261,30 @@ GemmChoice choose(const pe_gemm_desc& d, bool dl = false, int al = L_MN, int bl 
         // Long-K grids that need a K split with either tile: 128x128 tiles
         // split to about two blocks per CU, each split at least 16 slabs
         // deep, beat 64x64 tiles (config 5.3, ts,sp->tp float32 with K = 4096:
-        // 52.5 us against 57.1 us on one MI355X).
+        // 52.5 us against 57.1 us on one MI355X).  The split count is the one
+        // whose busiest CU does the least k work: blocks reach each XCD's
+        // cus / 8 CUs round robin, so its CUs run up to ceil(ceil(tiles * s /
+        // 8) / (cus / 8)) blocks of K / s (k rounded to slabs), a CU running
+        // one block at about 0.9 of the rate of two; ties go to fewer splits
+        // (fewer partials).  Against two blocks per CU, one MI355X: 768^2 x
+        // 4096 74.3 -> 55.0 us (14 splits), 1024 x 1536 x 4096 155.8 -> 116.9
+        // (8 splits).
         if (d.M > 64 && d.N > 64 && tiles128 < cus && d.split_k == 0 &&
             c.nbatch_total * d.M * d.N < (int64_t(1) << 32)) {
             const int64_t s2 = std::min<int64_t>(32, ceil_div(2 * cus, tiles128));
             if (d.K >= 16 * bk * s2) {
                 c.bm = 128;
-                long_k_split = s2;
+                const int64_t cpx = std::max<int64_t>(1, cus / 8);
+                double best_cost = 0.0;
+                for (int64_t sc = 2; sc <= std::min<int64_t>(32, d.K / (16 * bk)); ++sc) {
+                    const int64_t kps = ceil_div(ceil_div(d.K, sc), bk) * bk;
+                    const int64_t per_cu = ceil_div(ceil_div(tiles128 * ceil_div(d.K, kps), 8), cpx);
+                    const double cost = double(per_cu * kps) / (per_cu == 1 ? 0.9 : 1.0);
+                    if (long_k_split == 0 || cost < best_cost) {
+                        long_k_split = sc;
+                        best_cost = cost;
+                    }
+                }
             }
         }
         c.bn = c.bm;

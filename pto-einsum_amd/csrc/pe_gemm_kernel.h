@@ -207,9 +207,13 @@ struct TileLoader {
 };
 
 // Maps the block's n-th tile to (split, batch, tm, tn).  Blocks are dealt to
-// the 8 XCDs round-robin by block id, so XCD x = blockIdx % 8 is given the
-// contiguous logical range [x*T/8, (x+1)*T/8) -- tiles that share A rows and
-// B columns then meet in the same L2.  With fewer than 8 blocks, a plain
+// the 8 XCDs round-robin by block id, so XCD x = blockIdx % 8 runs
+// q + (x < r) of the G blocks (q = G / 8, r = G % 8) and is given a
+// contiguous logical range of the T tiles in proportion -- tiles that share A
+// rows and B columns then meet in the same L2, and with one block per tile
+// every block gets exactly one (equal ranges of T / 8 had left some blocks
+// two tiles and others none whenever G was not a multiple of 8: twice the
+// time for, e.g., 540 blocks).  With fewer than 8 blocks, a plain
 // grid-stride order is used.  Every logical tile is visited exactly once
 // whatever XCD actually runs the block.
 #ifndef PE_GEMM_XCD_WALK
@@ -222,10 +226,12 @@ struct TileWalk {
         if (G < 8 || !PE_GEMM_XCD_WALK) {
             next = b; end = total; step = G;
         } else {
-            const uint32_t x = b % 8, j = b / 8;
-            const uint32_t lo = uint32_t(uint64_t(x) * total / 8);
-            const uint32_t hi = uint32_t(uint64_t(x + 1) * total / 8);
-            next = lo + j; end = hi; step = (G - x + 7) / 8;
+            const uint32_t x = b % 8, j = b / 8, q = G / 8, r = G % 8;
+            // first tile of XCD y: its share of T after the blocks of XCDs 0 .. y-1
+            auto first = [&](uint32_t y) {
+                return uint32_t(uint64_t(total) * (uint64_t(y) * q + (y < r ? y : r)) / G);
+            };
+            next = first(x) + j; end = first(x + 1); step = q + (x < r ? 1u : 0u);
         }
     }
 };

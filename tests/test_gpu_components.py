@@ -379,3 +379,34 @@ def test_mfma_probe_runs_and_validates():
     assert lib.pe_probe_mfma(7, 0, 3, ctypes.c_void_p(out.data_ptr()), n, st) == -3
     assert lib.pe_probe_mfma(1, 0, 0, ctypes.c_void_p(out.data_ptr()), n, st) == -1
     assert lib.pe_probe_mfma(1, 0, 3, ctypes.c_void_p(out.data_ptr()), n - 1, st) == -2
+
+
+@pytest.mark.parametrize("split_k", [7, 9, 13, 15])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16], ids=["f32", "f16"])
+def test_tile_walk_with_block_counts_not_a_multiple_of_eight(split_k, dtype):
+    """36 tiles of 128x128 times an odd split count: grids of 252-540 blocks,
+    which the XCD-aware walk deals to the 8 XCDs in unequal shares; every
+    tile of every split is computed exactly once (the output starts as NaN)."""
+    M = N = 768
+    K = 4096 if dtype == torch.float32 else 8192
+    g = torch.Generator().manual_seed(split_k)
+    A = torch.randn(M, K, generator=g).to(dtype)
+    B = torch.randn(K, N, generator=g).to(dtype)
+    lib = abi.bind()
+    code = launch.DT_F32 if dtype == torch.float32 else launch.DT_F16
+    d = launch.GemmDesc(dtype=code, batch_shape=[1], a_bstride=[0], b_bstride=[0], c_bstride=[0],
+                        M=M, N=N, K=K, a_ms=K, a_ks=1, b_ks=N, b_ns=1, c_ms=N, c_ns=1, a_numel=M * K,
+                        b_numel=K * N, c_numel=M * N, tile=128, split_k=split_k)
+    cd = abi.gemm_desc(d)
+    ws_bytes = lib.pe_gemm_workspace_bytes(ctypes.byref(cd))
+    assert ws_bytes == split_k * M * N * 4
+    ws = torch.full((ws_bytes // 4,), float("nan"), device="cuda")
+    c = torch.full((M, N), float("nan"), device="cuda")
+    a, b = A.cuda(), B.cuda()
+    rc = lib.pe_gemm(ctypes.byref(cd), _ptr(a), _ptr(b), ctypes.c_void_p(c.data_ptr()), _ptr(ws), ws_bytes, _stream())
+    assert rc == 0, runtime.last_error()
+    got = c.cpu().double()
+    want = A.double() @ B.double()
+    bound = A.double().abs() @ B.double().abs()
+    assert not torch.isnan(got).any()
+    assert bool(((got - want).abs() <= 1e-5 * bound + 1e-6).all())
