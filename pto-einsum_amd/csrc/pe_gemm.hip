@@ -533,10 +533,13 @@ extern "C" int pe_gemm(const pe_gemm_desc* d, const void* a, const void* b, floa
     // against 88.1; fewer tiles lost: 1024 x 128 x 2048 16.9 against 18.7).
     // float16 split grids take its 64x64 tiles (float16 MFMAs are 16x the
     // float32 rate, so the split's partial round trip weighs more) when those
-    // give every CU one (K <= 8192) or a quarter of the CUs one (K <= 2048):
-    // 1024^3 19.9 -> 9.8 us, 768^2 x 2048 21.7 -> 12.6, 1024^2 x 8192 44.8 ->
-    // 37.6, 512^2 x 1024 12.7 -> 8.7; fewer tiles or longer K lost (256^2 x
-    // 2048 9.6 against 12.1, 4096 x 128 x 4096 22.6 against 26.4).
+    // give every CU one to three (K <= 8192) or a quarter of the CUs one (K <=
+    // 2048): 1024^3 19.9 -> 9.8 us, 768^2 x 2048 21.7 -> 12.6, 1024^2 x 8192
+    // 44.8 -> 37.6, 512^2 x 1024 12.7 -> 8.7, 2048 x 1024 x 1024 24.7 ->
+    // 17.0, 1152 x 2304 x 512 (2.5 per CU) 23.6 -> 19.3; fewer tiles, more
+    // tiles or longer K lost (256^2 x 2048 9.6 against 12.1, 4096 x 128 x
+    // 4096 22.6 against 26.4, 1664 x 2304 x 3072 with 3.7 tiles per CU 48.8
+    // against 60.1).
     const int64_t cus = cu_count();
     const int64_t tiles64 = nb * ceil_div(d->M, 64) * ceil_div(d->N, 64);
     const int64_t tiles32 = nb * ceil_div(d->M, 32) * ceil_div(d->N, 32);
@@ -547,8 +550,8 @@ extern "C" int pe_gemm(const pe_gemm_desc* d, const void* a, const void* b, floa
                                         : (d->K <= 2 * PE_GEMM_KS_MAX_K && ch.nsplit > 1 && tiles32 >= cus);
     } else {
         ks_tile = 64;
-        ks_k = ch.nsplit > 1 && ((tiles64 >= cus && d->K <= 8 * PE_GEMM_KS_MAX_K) ||
-                                 (4 * tiles64 >= cus && d->K <= 2 * PE_GEMM_KS_MAX_K));
+        ks_k = ch.nsplit > 1 && tiles64 <= 3 * cus &&
+               ((tiles64 >= cus && d->K <= 8 * PE_GEMM_KS_MAX_K) || (4 * tiles64 >= cus && d->K <= 2 * PE_GEMM_KS_MAX_K));
     }
     if (ks_k && dl && d->split_k == 0 && d->tile == 0 && gemm_ks_resident(d->dtype, al, bl, ks_tile) >= 1) {
         GemmArgs g{};
