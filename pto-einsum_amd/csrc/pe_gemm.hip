@@ -369,6 +369,51 @@ GemmChoice choose(const pe_gemm_desc& d, bool dl = false, int al = L_MN, int bl 
         split = std::min<int64_t>(split, std::max<int64_t>(ceil_div(cus, tiles), d.K / (16 * bk)));
         split = std::max<int64_t>(1, std::min<int64_t>(split, 32));
     }
+    if (d.dtype == PE_F32 && d.split_k == 0 && d.tile == 0 && c.bm == c.bn && (c.bm == 64 || c.bm == 128) &&
+        c.nbatch_total * d.M * d.N < (int64_t(1) << 32)) {
+        // Rebalance float32 square-tile grids the rules above leave uneven.
+        // Blocks reach each XCD's cus / 8 CUs round robin, so the busiest CU
+        // runs P = ceil(ceil(blocks / 8) / (cus / 8)) blocks; its time is
+        // modelled as P x (tile area) x (k per split), at 0.9 of the rate for
+        // 64x64 tiles and for a CU with one block, plus the split partials'
+        // round trip (0.01 per output element and split, per CU, in the same
+        // units: fitted to eight measured shapes, within 1 % of the best of
+        // their measured options on average).  Another tile or split count is
+        // taken only where the model gives it 20 % less time: 2304^2 x 6144
+        // 827.7 -> 580.4 us (128x128, 8 splits, against 1.27 unsplit tiles per
+        // CU), 384 x 2816 x 1536 74.5 -> 47.8 us (128x128, 6 splits, against
+        // 64x64 tiles unsplit) on one MI355X.
+        const int64_t cpx = std::max<int64_t>(1, cus / 8);
+        auto model = [&](int tile, int64_t sc) {
+            const int64_t kp = ceil_div(ceil_div(d.K, sc), bk) * bk;
+            const int64_t sp = ceil_div(d.K, kp);
+            const int64_t t = c.nbatch_total * ceil_div(d.M, tile) * ceil_div(d.N, tile);
+            const int64_t per = ceil_div(ceil_div(t * sp, 8), cpx);
+            const double eff = (tile == 64 ? 0.9 : 1.0) * (per == 1 ? 0.9 : 1.0);
+            const double area = double(tile / 64) * double(tile / 64);
+            const double part = sp > 1 ? 0.01 * double(sp) * double(c.nbatch_total * d.M * d.N) / double(cus) : 0.0;
+            return double(per) * area * double(kp) / eff + part;
+        };
+        const double now = model(c.bm, split);
+        double best = now;
+        int best_tile = c.bm;
+        int64_t best_split = split;
+        for (int tile : {64, 128}) {
+            if (tile == 128 && (d.M <= 64 || d.N <= 64)) continue;
+            for (int64_t sc = 1; sc <= std::min<int64_t>(32, std::max<int64_t>(1, d.K / (16 * bk))); ++sc) {
+                const double m = model(tile, sc);
+                if (m < best) {
+                    best = m;
+                    best_tile = tile;
+                    best_split = sc;
+                }
+            }
+        }
+        if (best < 0.8 * now) {
+            c.bm = c.bn = best_tile;
+            split = best_split;
+        }
+    }
     int64_t kps = ceil_div(ceil_div(d.K, split), bk) * bk;
     split = std::max<int64_t>(1, ceil_div(d.K, kps));
     c.nsplit = int(split);
