@@ -413,6 +413,36 @@ GemmChoice choose(const pe_gemm_desc& d, bool dl = false, int al = L_MN, int bl 
             c.bm = c.bn = best_tile;
             split = best_split;
         }
+    } else if (d.dtype == PE_F16 && d.split_k == 0 && d.tile == 0 && c.bm == 128 && c.bn == 128 && split == 1 &&
+               c.nbatch_total * d.M * d.N < (int64_t(1) << 32)) {
+        // float16 128x128 grids of one to four tiles per CU, unsplit: the
+        // same model with float16's own constants (a CU with one block at 0.8
+        // of the rate of two, partials 0.04 per output element and split:
+        // float16 MFMAs make the partials' round trip weigh more; fitted to
+        // twenty measured shapes) may split them where one round is left
+        // part-filled: 2816 x 1664 x 3072 68.9 -> 60.5 us with 4 splits.
+        const int64_t t = c.nbatch_total * ceil_div(d.M, 128) * ceil_div(d.N, 128);
+        if (t >= cus && t < 4 * cus) {
+            const int64_t cpx = std::max<int64_t>(1, cus / 8);
+            auto model = [&](int64_t sc) {
+                const int64_t kp = ceil_div(ceil_div(d.K, sc), bk) * bk;
+                const int64_t sp = ceil_div(d.K, kp);
+                const int64_t per = ceil_div(ceil_div(t * sp, 8), cpx);
+                const double part = sp > 1 ? 0.04 * double(sp) * double(c.nbatch_total * d.M * d.N) / double(cus) : 0.0;
+                return double(per) * 4.0 * double(kp) / (per == 1 ? 0.8 : 1.0) + part;
+            };
+            const double now = model(1);
+            double best = now;
+            int64_t best_split = 1;
+            for (int64_t sc = 2; sc <= std::min<int64_t>(32, d.K / (16 * bk)); ++sc) {
+                const double m = model(sc);
+                if (m < best) {
+                    best = m;
+                    best_split = sc;
+                }
+            }
+            if (best < 0.8 * now) split = best_split;
+        }
     }
     int64_t kps = ceil_div(ceil_div(d.K, split), bk) * bk;
     split = std::max<int64_t>(1, ceil_div(d.K, kps));
