@@ -1,0 +1,44 @@
+"""The GEMM tile / split choice, read on the CPU through pe_gemm_workspace_bytes
+(the workspace is nsplit x batches x M x N float32 partials, 0 when K is not
+split; with no GPU the library assumes MI355X's 256 CUs).  Pins the choices
+the measured tuning made: the busiest-CU split counts of long-K grids, the
+rebalancing of part-filled rounds, and the grids that must keep their choice
+(the benchmark configurations)."""
+import ctypes
+
+import pytest
+
+from pto_einsum import abi, launch
+
+
+def _splits(M, N, K, dtype="f32", nb=1):
+    code = launch.DT_F32 if dtype == "f32" else launch.DT_F16
+    d = launch.GemmDesc(dtype=code, batch_shape=[nb], a_bstride=[M * K], b_bstride=[K * N], c_bstride=[M * N],
+                        M=M, N=N, K=K, a_ms=K, a_ks=1, b_ks=N, b_ns=1, c_ms=N, c_ns=1,
+                        a_numel=nb * M * K, b_numel=nb * K * N, c_numel=nb * M * N)
+    ws = int(abi.bind().pe_gemm_workspace_bytes(ctypes.byref(abi.gemm_desc(d))))
+    assert ws % (nb * M * N * 4) == 0
+    return ws // (nb * M * N * 4)
+
+
+@pytest.mark.parametrize("shape,dtype,want", [
+    ((4096, 128, 4096), "f32", 16),      # config 5.3: 32 tiles of 128x128, two blocks per CU
+    ((768, 768, 4096), "f32", 14),       # 36 tiles: 504 blocks, 63 per XCD, two per CU
+    ((1024, 1536, 4096), "f32", 8),      # 96 tiles: 768 blocks, three per CU
+    ((2304, 2304, 6144), "f32", 7),      # 324 unsplit tiles left 1.27 per CU
+    ((2816, 1664, 3072), "f16", 4),      # float16, 286 unsplit tiles
+])
+def test_split_counts_of_uneven_grids(shape, dtype, want):
+    assert _splits(*shape, dtype=dtype) == want
+
+
+@pytest.mark.parametrize("shape,dtype,nb", [
+    ((1000, 1536, 777), "f32", 16),      # config 2: 768 tiles of 128x256, three per CU
+    ((2048, 2048, 128), "f16", 128),     # config 3's per-head products
+    ((4096, 4096, 128), "f16", 1),       # config 5.1
+    ((128, 128, 128), "f32", 256),       # the GDN contraction set, 16 x 16
+    ((8192, 8192, 8192), "f16", 1),      # the 256x256 float16 kernel
+    ((4096, 4096, 4096), "f32", 1),
+])
+def test_full_grids_stay_unsplit(shape, dtype, nb):
+    assert _splits(*shape, dtype=dtype, nb=nb) == 0
