@@ -63,6 +63,8 @@ struct ProductArgs {
     int64_t b_outer[kMaxOuter];
     int64_t a_inner, b_inner;
     int32_t nt;             // non-temporal output stores
+    int32_t a_flat;         // A's offset is the output's flat index (A laid out as the output)
+    int32_t b_first;        // outer axes below this index have B stride 0 (their index is unused)
 };
 
 template <typename E, int VEC>
@@ -155,14 +157,26 @@ __global__ __launch_bounds__(kThreads) void product_kernel(ProductArgs p) {
                 uint32_t row, colv;
                 p.inner_vecs.divmod(vv, row, colv);
                 uint32_t col = colv * VEC;
-                aoff = int64_t(col) * p.a_inner;
                 boff = int64_t(col) * p.b_inner;
-                for (int d = p.nouter - 1; d >= 0; --d) {
-                    uint32_t q, r;
-                    p.outer_div[d].divmod(row, q, r);
-                    aoff += int64_t(r) * p.a_outer[d];
-                    boff += int64_t(r) * p.b_outer[d];
-                    row = q;
+                if (p.a_flat) {
+                    // Only B's offset needs the outer indices, and only down
+                    // to its outermost axis with a nonzero stride.
+                    aoff = int64_t(vv) * VEC;
+                    for (int d = p.nouter - 1; d >= p.b_first; --d) {
+                        uint32_t q, r;
+                        p.outer_div[d].divmod(row, q, r);
+                        boff += int64_t(r) * p.b_outer[d];
+                        row = q;
+                    }
+                } else {
+                    aoff = int64_t(col) * p.a_inner;
+                    for (int d = p.nouter - 1; d >= 0; --d) {
+                        uint32_t q, r;
+                        p.outer_div[d].divmod(row, q, r);
+                        aoff += int64_t(r) * p.a_outer[d];
+                        boff += int64_t(r) * p.b_outer[d];
+                        row = q;
+                    }
                 }
             } else {
                 aoff = int64_t(vv) * VEC * p.a_inner;
@@ -293,6 +307,16 @@ int run(const pe_product_desc& d, const void* in0, const void* in1, float* out,
         args.a_outer[k] = sa[k];
         args.b_outer[k] = sb[k];
     }
+    // A flat: unit inner stride and every outer stride the extent product of
+    // the axes inside it, so A's element offset equals the output's.
+    int64_t flat = inner;
+    args.a_flat = nd > 0 && args.a_inner == 1;
+    for (int k = args.nouter - 1; k >= 0; --k) {
+        args.a_flat = args.a_flat && sa[k] == flat;
+        flat *= shape[k];
+    }
+    args.b_first = 0;
+    while (args.b_first < args.nouter && sb[args.b_first] == 0) ++args.b_first;
 
     // Vector path: VEC elements per lane along the innermost axis.  Four
     // elements give one 16-byte float32 store per lane, so each wave-wide
