@@ -12,9 +12,12 @@
 //  * the innermost destination axis is also source-contiguous: a streamed
 //    gather of contiguous runs with 16-byte vectors where the run length and
 //    strides allow it;
-//  * otherwise a 64x64 LDS-tiled transpose between the destination's
-//    innermost axis and the axis that is contiguous in the source, with the
-//    remaining axes decoded from blockIdx.  Both global sides are coalesced;
+//  * otherwise a 64x64 LDS-tiled transpose (32x32 for float32 destination
+//    rows that are not whole 16-byte vectors: [16, 777, 1000] -> (0, 2, 1)
+//    26.9 -> 24.0 us, while aligned rows measured equal or slower with the
+//    smaller tile) between the destination's innermost axis and the axis
+//    that is contiguous in the source, with the remaining axes decoded from
+//    blockIdx.  Both global sides are coalesced;
 //    the LDS tile has one padding column so the transposed read is free of
 //    bank conflicts.
 #include "pe_common.h"
@@ -122,7 +125,17 @@ struct TileArgs {
     int32_t nt;
 };
 
-constexpr int kTile = 64;
+// Tile edge: 64 elements, or 32 for float32 where the rule below picks it
+// (PE_TILE_SMALL_F32: 0 never, 1 when destination rows are not 16-byte
+// vectors, 2 always).
+#ifndef PE_TILE_SMALL_F32
+#define PE_TILE_SMALL_F32 1
+#endif
+template <typename W>
+int tile_edge(bool vstore) {
+    if (sizeof(W) != 4) return 64;
+    return (PE_TILE_SMALL_F32 == 2 || (PE_TILE_SMALL_F32 == 1 && !vstore)) ? 32 : 64;
+}
 
 // Permutation outputs from this size on are written with non-temporal
 // stores.  Lower than the GEMM / product threshold: a 67 MB gather ran 6 %
@@ -146,13 +159,15 @@ constexpr int kTile = 64;
 // banks.  Tiles are walked diagonally (the q-tile index is offset by the
 // p-tile index), so concurrently running blocks do not all write rows that
 // are a large power of two apart in the same column range.
-template <typename W, bool VLOAD, bool VSTORE>
+template <typename W, bool VLOAD, bool VSTORE, int kTile = 64>
 __global__ __launch_bounds__(kThreads) void tile_transpose_kernel(TileArgs p) {
     constexpr int VEC = 16 / sizeof(W);
     constexpr int LVPR = VLOAD ? kTile / VEC : kTile;   // lanes per tile row, read side
     constexpr int LW = VLOAD ? VEC : 1;                  // elements per lane access, read
     constexpr int SVPR = VSTORE ? kTile / VEC : kTile;  // lanes per tile row, write side
     constexpr int SW = VSTORE ? VEC : 1;
+    static_assert(kTile % (kThreads / LVPR) == 0 && kTile % (kThreads / SVPR) == 0 && kTile >= kThreads / LVPR &&
+                  kTile >= kThreads / SVPR, "tile rows must split evenly over the block's passes");
     __shared__ W tile[kTile][kTile + 1];  // tile[q][p]
     const W* __restrict__ src = static_cast<const W*>(p.src);
     W* __restrict__ dst = static_cast<W*>(p.dst);
@@ -326,8 +341,9 @@ int run(const pe_permute_desc& d, const void* src, void* dst, hipStream_t s) {
     t.P = shape[pax]; t.Q = shape[qax];
     t.src_q_stride = sst[qax];
     t.dst_p_stride = dst_stride[pax];
-    t.tiles_p = uint32_t(ceil_div(t.P, kTile));
-    t.tiles_q = uint32_t(ceil_div(t.Q, kTile));
+    const int edge = tile_edge<W>(aligned(dst, 16) && t.dst_p_stride % (16 / int(sizeof(W))) == 0);
+    t.tiles_p = uint32_t(ceil_div(t.P, edge));
+    t.tiles_q = uint32_t(ceil_div(t.Q, edge));
     int nb = 0;
     int64_t nbt = 1;
     for (int k = 0; k < nd; ++k) {
@@ -350,6 +366,14 @@ int run(const pe_permute_desc& d, const void* src, void* dst, hipStream_t s) {
     }
     int64_t tiles = int64_t(t.tiles_p) * t.tiles_q * nbt;
     const dim3 grid(grid_cap(tiles, PE_TILE_GRID_PER_CU));
+    if constexpr (sizeof(W) == 4) if (edge == 32) {
+        if (vload && vstore) hipLaunchKernelGGL((tile_transpose_kernel<W, true, true, 32>), grid, dim3(kThreads), 0, s, t);
+        else if (vload) hipLaunchKernelGGL((tile_transpose_kernel<W, true, false, 32>), grid, dim3(kThreads), 0, s, t);
+        else if (vstore) hipLaunchKernelGGL((tile_transpose_kernel<W, false, true, 32>), grid, dim3(kThreads), 0, s, t);
+        else hipLaunchKernelGGL((tile_transpose_kernel<W, false, false, 32>), grid, dim3(kThreads), 0, s, t);
+        PE_CHECK_HIP(hipGetLastError());
+        return PE_OK;
+    }
     if (vload && vstore) hipLaunchKernelGGL((tile_transpose_kernel<W, true, true>), grid, dim3(kThreads), 0, s, t);
     else if (vload) hipLaunchKernelGGL((tile_transpose_kernel<W, true, false>), grid, dim3(kThreads), 0, s, t);
     else if (vstore) hipLaunchKernelGGL((tile_transpose_kernel<W, false, true>), grid, dim3(kThreads), 0, s, t);

@@ -410,3 +410,63 @@ def test_tile_walk_with_block_counts_not_a_multiple_of_eight(split_k, dtype):
     bound = A.double().abs() @ B.double().abs()
     assert not torch.isnan(got).any()
     assert bool(((got - want).abs() <= 1e-5 * bound + 1e-6).all())
+
+
+# pe_product stride patterns: operand A laid out as the output (its offset is
+# the flat index) with B broadcast over outer axes in every position, and A
+# transposed or broadcast itself (the general per-axis decode).
+PRODUCT_STRIDES = [
+    # out shape, a strides, b strides
+    ((3, 40, 5, 64), (12800, 320, 64, 1), (0, 64, 0, 1)),        # bshd,sd->bshd: B's outermost axis broadcast
+    ((3, 40, 5, 64), (12800, 320, 64, 1), (320, 0, 64, 1)),      # B broadcast over the second axis only
+    ((3, 40, 5, 64), (12800, 320, 64, 1), (0, 0, 0, 1)),         # B a row, every outer axis broadcast
+    ((3, 40, 5, 64), (12800, 320, 64, 1), (12800, 320, 64, 0)),  # B broadcast along the vector axis
+    ((3, 40, 5, 64), (12800, 320, 64, 1), (0, 5, 1, 200)),       # B transposed: scalar path
+    ((6, 40, 64), (64, 384, 1), (0, 64, 1)),                      # A with permuted outer axes
+    ((6, 40, 64), (0, 64, 1), (2560, 64, 1)),                     # A broadcast, B laid out as the output
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+@pytest.mark.parametrize("add_zero", [0, 1])
+@pytest.mark.parametrize("shape,sa,sb", PRODUCT_STRIDES)
+def test_product_stride_patterns_bit_exact(shape, sa, sb, add_zero, dtype):
+    g = torch.Generator().manual_seed(len(shape) * 7 + sum(sb) + add_zero)
+    na = 1 + sum((n - 1) * s for n, s in zip(shape, sa))
+    nb = 1 + sum((n - 1) * s for n, s in zip(shape, sb))
+    a = torch.randn(na, generator=g).to(dtype)
+    b = torch.randn(nb, generator=g).to(dtype)
+    a[::7] = -0.0
+    nout = int(np.prod(shape))
+    code = launch.DT_F32 if dtype == torch.float32 else launch.DT_F16
+    d = abi.product_desc(launch.ProductDesc(code, add_zero, list(shape), list(sa), list(sb), na, nb))
+    ga, gb = a.cuda(), b.cuda()
+    out = torch.full((nout,), float("nan"), device="cuda")
+    rc = abi.bind().pe_product(ctypes.byref(d), _ptr(ga), _ptr(gb), _ptr(out), _stream())
+    assert rc == 0, runtime.last_error()
+    av = torch.as_strided(a, shape, sa).float()
+    bv = torch.as_strided(b, shape, sb).float()
+    want = av * bv
+    if add_zero:
+        want = 0.0 + want
+    got = out.cpu().view(shape)
+    assert torch.equal(got.view(torch.int32), want.contiguous().view(torch.int32))
+
+
+@pytest.mark.parametrize("shape,perm", [((16, 777, 1000), (0, 2, 1)),   # config 2 in0: 32-element float32 tiles
+                                        ((3, 37, 45), (0, 2, 1)),       # partial tiles on both axes
+                                        ((2, 5, 33, 7), (0, 3, 2, 1)),  # odd rows, batch axes
+                                        ((65, 31), (1, 0))])
+def test_float32_transposes_with_unaligned_destination_rows(shape, perm):
+    """Destination rows that are not whole 16-byte vectors take the
+    32-element float32 tile; bit-exact against torch.permute (NaN payloads
+    included, the data being arbitrary 32-bit patterns)."""
+    n = int(np.prod(shape))
+    src = torch.randint(-2**31, 2**31 - 1, (n,), dtype=torch.int32, device="cuda")
+    dst = torch.zeros(n, dtype=torch.int32, device="cuda")
+    from pto_einsum.planner import transpose_config
+    cfg = transpose_config("p", shape, perm)
+    d = abi.permute_desc(launch.PermuteDesc(4, list(cfg["to_shape"]), list(cfg["perm_strides"]), n))
+    rc = abi.bind().pe_permute(ctypes.byref(d), _ptr(src), _ptr(dst), _stream())
+    assert rc == 0, runtime.last_error()
+    assert torch.equal(dst.cpu(), src.cpu().view(shape).permute(perm).contiguous().view(-1))
