@@ -13,7 +13,8 @@
 //    gather of contiguous runs with 16-byte vectors where the run length and
 //    strides allow it;
 //  * otherwise a 64x64 LDS-tiled transpose (32x32 for float32 destination
-//    rows that are not whole 16-byte vectors: [16, 777, 1000] -> (0, 2, 1)
+//    rows that are not whole 16-byte vectors, 32x64 where those rows are
+//    33 to 64 elements long: [16, 777, 1000] -> (0, 2, 1)
 //    26.9 -> 24.0 us, while aligned rows measured equal or slower with the
 //    smaller tile) between the destination's innermost axis and the axis
 //    that is contiguous in the source, with the remaining axes decoded from
@@ -131,6 +132,7 @@ struct TileArgs {
 #ifndef PE_TILE_SMALL_F32
 #define PE_TILE_SMALL_F32 1
 #endif
+
 template <typename W>
 int tile_edge(bool vstore) {
     if (sizeof(W) != 4) return 64;
@@ -159,16 +161,16 @@ int tile_edge(bool vstore) {
 // banks.  Tiles are walked diagonally (the q-tile index is offset by the
 // p-tile index), so concurrently running blocks do not all write rows that
 // are a large power of two apart in the same column range.
-template <typename W, bool VLOAD, bool VSTORE, int kTile = 64>
+template <typename W, bool VLOAD, bool VSTORE, int TP = 64, int TQ = TP>
 __global__ __launch_bounds__(kThreads) void tile_transpose_kernel(TileArgs p) {
     constexpr int VEC = 16 / sizeof(W);
-    constexpr int LVPR = VLOAD ? kTile / VEC : kTile;   // lanes per tile row, read side
+    constexpr int LVPR = VLOAD ? TP / VEC : TP;   // lanes per tile row, read side
     constexpr int LW = VLOAD ? VEC : 1;                  // elements per lane access, read
-    constexpr int SVPR = VSTORE ? kTile / VEC : kTile;  // lanes per tile row, write side
+    constexpr int SVPR = VSTORE ? TQ / VEC : TQ;  // lanes per tile row, write side
     constexpr int SW = VSTORE ? VEC : 1;
-    static_assert(kTile % (kThreads / LVPR) == 0 && kTile % (kThreads / SVPR) == 0 && kTile >= kThreads / LVPR &&
-                  kTile >= kThreads / SVPR, "tile rows must split evenly over the block's passes");
-    __shared__ W tile[kTile][kTile + 1];  // tile[q][p]
+    static_assert(TQ % (kThreads / LVPR) == 0 && TP % (kThreads / SVPR) == 0 && TQ >= kThreads / LVPR &&
+                  TP >= kThreads / SVPR, "tile rows must split evenly over the block's passes");
+    __shared__ W tile[TQ][TP + 1];  // tile[q][p]
     const W* __restrict__ src = static_cast<const W*>(p.src);
     W* __restrict__ dst = static_cast<W*>(p.dst);
     const uint32_t tiles_per_batch = p.tiles_p * p.tiles_q;
@@ -189,10 +191,10 @@ __global__ __launch_bounds__(kThreads) void tile_transpose_kernel(TileArgs p) {
             dbase += int64_t(r) * p.batch_dst[d];
             bidx = q;
         }
-        const int64_t p0 = int64_t(tp) * kTile, q0 = int64_t(tq) * kTile;
+        const int64_t p0 = int64_t(tp) * TP, q0 = int64_t(tq) * TQ;
         // Read: tile rows are q, each lane covers LW consecutive p.
 #pragma unroll
-        for (int it = 0; it < kTile / (kThreads / LVPR); ++it) {
+        for (int it = 0; it < TQ / (kThreads / LVPR); ++it) {
             const int r = lr + it * (kThreads / LVPR);
             const int64_t gq = q0 + r, gp = p0 + lc * LW;
             if (gq >= p.Q) continue;
@@ -210,7 +212,7 @@ __global__ __launch_bounds__(kThreads) void tile_transpose_kernel(TileArgs p) {
         __syncthreads();
         // Write: destination rows are p, each lane covers SW consecutive q.
 #pragma unroll
-        for (int it = 0; it < kTile / (kThreads / SVPR); ++it) {
+        for (int it = 0; it < TP / (kThreads / SVPR); ++it) {
             const int r = sr + it * (kThreads / SVPR);
             const int64_t gp = p0 + r, gq = q0 + sc * SW;
             if (gp >= p.P) continue;
@@ -250,6 +252,14 @@ __global__ __launch_bounds__(kThreads) void gather_wide_kernel(const W* __restri
 int grid_cap(int64_t blocks, int per_cu = 16) {
     int64_t cap = int64_t(cu_count()) * per_cu;
     return int(std::max<int64_t>(1, std::min(blocks, cap)));
+}
+
+template <typename W, int TP, int TQ>
+void launch_tile(bool vload, bool vstore, dim3 grid, hipStream_t s, const TileArgs& t) {
+    if (vload && vstore) hipLaunchKernelGGL((tile_transpose_kernel<W, true, true, TP, TQ>), grid, dim3(kThreads), 0, s, t);
+    else if (vload) hipLaunchKernelGGL((tile_transpose_kernel<W, true, false, TP, TQ>), grid, dim3(kThreads), 0, s, t);
+    else if (vstore) hipLaunchKernelGGL((tile_transpose_kernel<W, false, true, TP, TQ>), grid, dim3(kThreads), 0, s, t);
+    else hipLaunchKernelGGL((tile_transpose_kernel<W, false, false, TP, TQ>), grid, dim3(kThreads), 0, s, t);
 }
 
 template <typename W>
@@ -342,8 +352,12 @@ int run(const pe_permute_desc& d, const void* src, void* dst, hipStream_t s) {
     t.src_q_stride = sst[qax];
     t.dst_p_stride = dst_stride[pax];
     const int edge = tile_edge<W>(aligned(dst, 16) && t.dst_p_stride % (16 / int(sizeof(W))) == 0);
-    t.tiles_p = uint32_t(ceil_div(t.P, edge));
-    t.tiles_q = uint32_t(ceil_div(t.Q, edge));
+    // The small tile spans q with 64 where that covers q in one tile
+    // ([64, 37, 4000] -> (0, 2, 1): 27.3 -> 19.1 us; 32 x 64 and 64 x 32
+    // tiles were otherwise equal or slower than 32 x 32).
+    const int tp = edge, tq = edge == 32 && t.Q > 32 && t.Q <= 64 ? 64 : edge;
+    t.tiles_p = uint32_t(ceil_div(t.P, tp));
+    t.tiles_q = uint32_t(ceil_div(t.Q, tq));
     int nb = 0;
     int64_t nbt = 1;
     for (int k = 0; k < nd; ++k) {
@@ -366,18 +380,13 @@ int run(const pe_permute_desc& d, const void* src, void* dst, hipStream_t s) {
     }
     int64_t tiles = int64_t(t.tiles_p) * t.tiles_q * nbt;
     const dim3 grid(grid_cap(tiles, PE_TILE_GRID_PER_CU));
-    if constexpr (sizeof(W) == 4) if (edge == 32) {
-        if (vload && vstore) hipLaunchKernelGGL((tile_transpose_kernel<W, true, true, 32>), grid, dim3(kThreads), 0, s, t);
-        else if (vload) hipLaunchKernelGGL((tile_transpose_kernel<W, true, false, 32>), grid, dim3(kThreads), 0, s, t);
-        else if (vstore) hipLaunchKernelGGL((tile_transpose_kernel<W, false, true, 32>), grid, dim3(kThreads), 0, s, t);
-        else hipLaunchKernelGGL((tile_transpose_kernel<W, false, false, 32>), grid, dim3(kThreads), 0, s, t);
-        PE_CHECK_HIP(hipGetLastError());
-        return PE_OK;
+    if constexpr (sizeof(W) == 4) {
+        if (tp == 32 && tq == 64) launch_tile<W, 32, 64>(vload, vstore, grid, s, t);
+        else if (tp == 32) launch_tile<W, 32, 32>(vload, vstore, grid, s, t);
+        else launch_tile<W, 64, 64>(vload, vstore, grid, s, t);
+    } else {
+        launch_tile<W, 64, 64>(vload, vstore, grid, s, t);
     }
-    if (vload && vstore) hipLaunchKernelGGL((tile_transpose_kernel<W, true, true>), grid, dim3(kThreads), 0, s, t);
-    else if (vload) hipLaunchKernelGGL((tile_transpose_kernel<W, true, false>), grid, dim3(kThreads), 0, s, t);
-    else if (vstore) hipLaunchKernelGGL((tile_transpose_kernel<W, false, true>), grid, dim3(kThreads), 0, s, t);
-    else hipLaunchKernelGGL((tile_transpose_kernel<W, false, false>), grid, dim3(kThreads), 0, s, t);
     PE_CHECK_HIP(hipGetLastError());
     return PE_OK;
 }

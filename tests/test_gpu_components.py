@@ -456,10 +456,12 @@ def test_product_stride_patterns_bit_exact(shape, sa, sb, add_zero, dtype):
 @pytest.mark.parametrize("shape,perm", [((16, 777, 1000), (0, 2, 1)),   # config 2 in0: 32-element float32 tiles
                                         ((3, 37, 45), (0, 2, 1)),       # partial tiles on both axes
                                         ((2, 5, 33, 7), (0, 3, 2, 1)),  # odd rows, batch axes
-                                        ((65, 31), (1, 0))])
+                                        ((65, 31), (1, 0)),
+                                        ((64, 37, 400), (0, 2, 1)),     # q = 37: one 32 x 64 tile spans it
+                                        ((5, 50, 70), (0, 2, 1))])
 def test_float32_transposes_with_unaligned_destination_rows(shape, perm):
     """Destination rows that are not whole 16-byte vectors take the
-    32-element float32 tile; bit-exact against torch.permute (NaN payloads
+    32-element float32 tile (32 x 64 where q is 33 to 64); bit-exact against torch.permute (NaN payloads
     included, the data being arbitrary 32-bit patterns)."""
     n = int(np.prod(shape))
     src = torch.randint(-2**31, 2**31 - 1, (n,), dtype=torch.int32, device="cuda")
