@@ -133,6 +133,13 @@ struct TileArgs {
 #define PE_TILE_SMALL_F32 1
 #endif
 
+// Float16 tile extents along p and q.
+#ifndef PE_TILE_F16_P
+#define PE_TILE_F16_P 64
+#endif
+#ifndef PE_TILE_F16_Q
+#define PE_TILE_F16_Q 64
+#endif
 template <typename W>
 int tile_edge(bool vstore) {
     if (sizeof(W) != 4) return 64;
@@ -355,7 +362,8 @@ int run(const pe_permute_desc& d, const void* src, void* dst, hipStream_t s) {
     // The small tile spans q with 64 where that covers q in one tile
     // ([64, 37, 4000] -> (0, 2, 1): 27.3 -> 19.1 us; 32 x 64 and 64 x 32
     // tiles were otherwise equal or slower than 32 x 32).
-    const int tp = edge, tq = edge == 32 && t.Q > 32 && t.Q <= 64 ? 64 : edge;
+    const int tp = sizeof(W) == 2 ? PE_TILE_F16_P : edge;
+    const int tq = sizeof(W) == 2 ? PE_TILE_F16_Q : (edge == 32 && t.Q > 32 && t.Q <= 64 ? 64 : edge);
     t.tiles_p = uint32_t(ceil_div(t.P, tp));
     t.tiles_q = uint32_t(ceil_div(t.Q, tq));
     int nb = 0;
@@ -385,7 +393,7 @@ int run(const pe_permute_desc& d, const void* src, void* dst, hipStream_t s) {
         else if (tp == 32) launch_tile<W, 32, 32>(vload, vstore, grid, s, t);
         else launch_tile<W, 64, 64>(vload, vstore, grid, s, t);
     } else {
-        launch_tile<W, 64, 64>(vload, vstore, grid, s, t);
+        launch_tile<W, PE_TILE_F16_P, PE_TILE_F16_Q>(vload, vstore, grid, s, t);
     }
     PE_CHECK_HIP(hipGetLastError());
     return PE_OK;
