@@ -8,13 +8,17 @@ steps (2*b*i*j*k flops per step).  ``roofline`` relates the GEMM kernel's
 average launch time (HIP events recorded around each launch on the launch
 stream) to the float32 MFMA peak.  ``cpu_baseline`` times the reference CPU
 route (cpu_einsum.h compiled by oracle/ref_build.py; the C restatement in
-oracle/ when that build is absent) on the whole of config 2, one thread.
+oracle/ when that build is absent) on the whole of config 2, one thread, and
+every ``per_config`` row carries the same route's time on that config
+(``cpu_s``, one thread, same seeded inputs up-cast to float32).
 
 Cache: MI355X has a 256 MB Infinity Cache in front of HBM.  Every timed case
 therefore rotates through enough copies of its operands and output (at least
-1 GiB in total, four times the cache) that each call reads operands no call
-has touched for over 768 MB of traffic: the figures are HBM figures, not
-cache figures.  The headline steps rotate the same way.
+1 GiB in total, four times the cache) that each call reads operands and
+writes an output no call has touched for over 768 MB of traffic: the figures
+are HBM figures, not cache figures.  Einsum cases call the per-shape
+library's run_einsum_exec with an explicit output per operand set; the
+headline steps rotate the same way.
 
 ``per_config`` adds every other benchmark equation at full size with its own
 binding roof (HBM bytes or MFMA flops).  Those kernels run for tens of
@@ -31,6 +35,13 @@ operand rotation as the ``per_config`` rows.
 ``gdn`` times the GDN contraction set at the reference's sizes the same way,
 and ``gdn_stages`` two of its stage sequences issued eagerly (one Python call
 per launch) and replayed as one HIP graph (``pto_einsum.StageGraph``).
+
+``launch_floor`` replays the launch probe (one wave, one store) in a graph
+of as many launches as config 1's rotation: the fixed cost of a launch that
+config 1's 256^3 GEMM is read against.  ``cold_call`` gives the host cost of
+the one-shot ``einsum()``: the first call on a new shape (plan, host-code
+compile, load), the first after the in-process runner cache is cleared, and
+a cached call's host time.
 
 ``roofline.traffic`` (HBM bytes per launch of the headline GEMM) is read from
 profiles/gemm_f32_config2_traffic.json, written from two rocprofv3 --pmc runs
@@ -353,6 +364,32 @@ class Case:
         self.name, self.prepare, self.finish = name, prepare, finish
 
 
+def exec_call(builder, dev):
+    """call(x, y, out): one run_einsum_exec of the built per-shape library
+    (the C ABI the reference's runner calls, builder.py:877-881) on the
+    current stream, writing into `out`, with one workspace kept with the
+    call.  Every rotated operand set carries its own output, so no
+    two calls in a row write the same output buffer."""
+    import torch
+
+    lib, ct = builder.lib, builder.c_type
+    ws = torch.zeros(max(int(builder._ws_bytes), 256), dtype=torch.uint8, device=dev)
+    swap = builder._swap_operands
+
+    def call(x, y, out):
+        a, b = (y, x) if swap else (x, y)
+        rc = lib.run_einsum_exec(ctypes.cast(a.data_ptr(), ctypes.POINTER(ct)),
+                                 ctypes.cast(b.data_ptr(), ctypes.POINTER(ct)),
+                                 ctypes.cast(out.data_ptr(), ctypes.POINTER(ctypes.c_float)),
+                                 ctypes.c_void_p(ws.data_ptr()),
+                                 ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        if rc != 0:
+            raise RuntimeError(f"run_einsum_exec failed ({rc})")
+
+    call.workspace = ws
+    return call
+
+
 def einsum_case(name, eq, gen, dt, seed, label=None):
     import torch
 
@@ -362,12 +399,16 @@ def einsum_case(name, eq, gen, dt, seed, label=None):
         g = torch.Generator().manual_seed(seed)
         x, y = gen(g)
         x, y = x.to(dev), y.to(dev)
-        r = EinsumBuilder(eq, [tuple(x.shape), tuple(y.shape)], x.dtype).build()
-        out_bytes = r(x, y).numel() * 4
-        return r, (x, y), x.numel() * x.element_size() + y.numel() * y.element_size() + out_bytes
+        builder = EinsumBuilder(eq, [tuple(x.shape), tuple(y.shape)], x.dtype)
+        builder.build()
+        out = torch.empty(builder.recipe["out_shape"], dtype=torch.float32, device=dev)
+        call = exec_call(builder, dev)
+        call.builder = builder
+        return call, (x, y, out), (x.numel() * x.element_size() + y.numel() * y.element_size()
+                                    + out.numel() * 4)
 
     def finish(ms, operands, nsets):
-        x, y = operands
+        x, y = operands[:2]
         f, nb = work(eq, x, y)
         rf, tf, gb = roofline(f, nb, ms, dt)
         row = dict(config=name, equation=eq, dtype=dt, us=round(ms * 1e3, 2), tflops=round(tf, 3),
@@ -378,7 +419,9 @@ def einsum_case(name, eq, gen, dt, seed, label=None):
             f"{rf['bound']} {rf['frac'] * 100:.1f}%  ({nsets} rotated sets)")
         return row
 
-    return Case(name, prepare, finish)
+    case = Case(name, prepare, finish)
+    case.seed, case.gen, case.eq = seed, gen, eq
+    return case
 
 
 def transpose_case(label, eq, shapes, dtype, entry):
@@ -456,12 +499,13 @@ def chain_case(precise):
         k = (torch.randn(S, N, generator=g) * N ** -0.5).half().to(dev)
         v = torch.randn(S, P, generator=g).half().to(dev)
         m = decay(T, 0.995).to(dev)
+        out = torch.empty((T, P), dtype=torch.float32, device=dev)
         nbytes = (q.numel() + k.numel() + v.numel()) * 2 + m.numel() * 4 + T * P * 4
 
-        def call(q, k, v, m):
-            linear_attention(q, k, v, m, precise=precise)
+        def call(q, k, v, m, out):
+            linear_attention(q, k, v, m, precise=precise, out=out)
 
-        return call, (q, k, v, m), nbytes
+        return call, (q, k, v, m, out), nbytes
 
     def finish(ms, operands, nsets):
         flops = 2 * T * S * N + T * S + 2 * T * S * P
@@ -554,12 +598,20 @@ def gdn_cases():
     return out
 
 
+HEADLINE_SEED = 2
+
+
+def headline_gen(g):
+    """Config 2's operands: standard normal, b=16, j=777, i=1000, k=1536."""
+    import torch
+
+    return torch.randn((16, 777, 1000), generator=g), torch.randn((16, 777, 1536), generator=g)
+
+
 def all_cases():
     import torch
 
-    head = einsum_case("2", "bji,bjk->bik",
-                       lambda g: (torch.randn((16, 777, 1000), generator=g), torch.randn((16, 777, 1536), generator=g)),
-                       "f32", 2)
+    head = einsum_case("2", "bji,bjk->bik", headline_gen, "f32", HEADLINE_SEED)
     groups = {"headline": [head],
               "per_config": [einsum_case(n, e, gen, d, 100 + i) for i, (n, e, gen, d) in enumerate(config_list())]
               + [chain_case(False), chain_case(True)],
@@ -759,24 +811,15 @@ def time_torch_thin(dev, calls=50):
 # ------------------------------------------------------------ CPU baseline --
 
 def cpu_baseline(budget_s=10.0):
-    """Reference CPU route on the whole of config 2 (all 16 batches), one
-    thread: called until `budget_s` is spent (at least once); best call."""
+    """Reference CPU route on the whole of config 2 (all 16 batches) with the
+    headline's own inputs (same generator and seed), one thread: called
+    until `budget_s` is spent (at least once); best call."""
     import torch
 
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import oracle
-    import ref_build
-
     eq, s0, s1 = "bji,bjk->bik", (16, 777, 1000), (16, 777, 1536)
-    g = torch.Generator().manual_seed(1)
-    a = torch.randn(s0, generator=g).numpy()
-    b = torch.randn(s1, generator=g).numpy()
-    if os.path.exists(ref_build.so_path(eq, s0, s1)):
-        kind = "reference"
-        fn = lambda: ref_build.run(eq, a, b)  # noqa: E731
-    else:
-        kind = "port"
-        fn = lambda: oracle.einsum(eq, a, b)  # noqa: E731
+    g = torch.Generator().manual_seed(HEADLINE_SEED)
+    a, b = (t.numpy() for t in headline_gen(g))
+    fn, kind = _cpu_route(eq, a, b)
     times = []
     t_start = time.perf_counter()
     while not times or (time.perf_counter() - t_start) + statistics.median(times) < budget_s:
@@ -786,10 +829,176 @@ def cpu_baseline(budget_s=10.0):
     dt = min(times)
     flops = 2.0 * 16 * 1000 * 1536 * 777
     return dict(value=round(flops / dt / 1e12, 6), unit="TFLOP/s", cores=1, kind=kind,
-                sample=(f"the whole of config 2 (bji,bjk->bik float32, b=16, j=777, i=1000, k=1536), "
-                        f"{flops / 1e9:.1f} GFLOP per call, {len(times)} call(s) in {sum(times):.1f} s; "
-                        f"best call {dt:.2f} s on 1 thread of {os.cpu_count()}"),
+                sample=(f"the whole of config 2 (bji,bjk->bik float32, b=16, j=777, i=1000, k=1536; the "
+                        f"headline's seeded inputs), {flops / 1e9:.1f} GFLOP per call, {len(times)} call(s) in "
+                        f"{sum(times):.1f} s; best call {dt:.2f} s on 1 thread of {os.cpu_count()}"),
                 seconds=round(sum(times), 3))
+
+
+def _cpu_route(eq, a, b):
+    """(callable, kind) running the reference CPU route on float32 arrays:
+    the reference's own cpu_einsum.h build (oracle/_ref) when it was built
+    for these shapes, else the C restatement in oracle/."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+    import ref_build
+
+    if os.path.exists(ref_build.so_path(eq, a.shape, b.shape)):
+        return (lambda: ref_build.run(eq, a, b)), "reference"
+    return (lambda: oracle.einsum(eq, a, b)), "port"
+
+
+def _cpu_time(fn):
+    """Median wall time (s) of one synchronous call: three calls when one
+    takes under 3 s, else the single call."""
+    t = time.perf_counter()
+    fn()
+    first = time.perf_counter() - t
+    if first >= 3.0:
+        return first, 1
+    times = [first]
+    for _ in range(2):
+        t = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t)
+    return statistics.median(times), 3
+
+
+def cpu_per_config(per_config_rows, cases):
+    """The reference CPU route (device="cpu": float32, one thread) on every
+    per-config workload at full size, with the inputs the GPU row used (same
+    generator and seed; float16 inputs up-cast to float32, as that route is
+    float32-only, builder.py:612-613).  Adds cpu_s, cpu_cores, cpu_kind and
+    cpu_calls to each row; the fused chain's row gets the three reference
+    einsums it replaces run in sequence on its own inputs."""
+    import torch
+
+    host = os.cpu_count()
+    by_name = {c.name: c for c in cases}
+    for row in per_config_rows:
+        name = row["config"]
+        if name.startswith("5.F"):
+            continue
+        case = by_name[name]
+        g = torch.Generator().manual_seed(case.seed)
+        x, y = case.gen(g)
+        a, b = x.float().numpy(), y.float().numpy()
+        fn, kind = _cpu_route(case.eq, a, b)
+        dt, calls = _cpu_time(fn)
+        row.update(cpu_s=round(dt, 4), cpu_cores=f"1 of {host}", cpu_kind=kind, cpu_calls=calls)
+        log(f"bench: cpu {name} {case.eq} {dt:.3f} s ({kind}, {calls} call(s), 1 thread of {host})")
+    chain = [r for r in per_config_rows if r["config"].startswith("5.F")]
+    if chain:
+        g = torch.Generator().manual_seed(105)
+        T = S = T5
+        q = (torch.randn(T, N5, generator=g) * N5 ** -0.5).half().float().numpy()
+        k = (torch.randn(S, N5, generator=g) * N5 ** -0.5).half().float().numpy()
+        v = torch.randn(S, N5, generator=g).half().float().numpy()
+        m = decay(T, 0.995).numpy()
+        f1, kind = _cpu_route("tn,sn->ts", q, k)
+
+        def steps():
+            A = f1()
+            A2 = _cpu_route("ts,ts->ts", A, m)[0]()
+            return _cpu_route("ts,sp->tp", A2, v)[0]()
+
+        dt, calls = _cpu_time(steps)
+        for r in chain:
+            r.update(cpu_s=round(dt, 4), cpu_cores=f"1 of {host}", cpu_kind=kind, cpu_calls=calls,
+                     cpu_note="the three reference einsums tn,sn->ts, ts,ts->ts, ts,sp->tp in sequence")
+        log(f"bench: cpu 5.F (three einsums) {dt:.3f} s ({kind}, {calls} call(s))")
+
+
+def cold_call(dev):
+    """Host cost of the one-shot einsum() (builder.py:887-902 re-plans and
+    re-loads per call): the first call on a new shape with an empty build
+    directory (plan, host-code generation and compile, library load,
+    workspace), the first call after the in-process runner cache is cleared
+    (plan and load from the on-disk cache), and the steady-state host time
+    of a cached call (Python checks, output allocation, ctypes launch),
+    measured without synchronising, beside the GPU time of the same call."""
+    import shutil
+    import tempfile
+
+    import torch
+
+    from pto_einsum import builder as pb
+    from pto_einsum import einsum
+
+    g = torch.Generator().manual_seed(99)
+    a = torch.rand(256, 257, generator=g).to(dev)
+    b = torch.rand(257, 255, generator=g).to(dev)
+    eq = "ij,jk->ik"
+    tmp = tempfile.mkdtemp(prefix="pe_cold_")
+    old = os.environ.get("EINSUM_BUILD_DIR")
+    os.environ["EINSUM_BUILD_DIR"] = tmp
+    try:
+        pb.clear_runner_cache()
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        einsum(eq, a, b)
+        torch.cuda.synchronize()
+        first = time.perf_counter() - t
+        pb.clear_runner_cache()
+        t = time.perf_counter()
+        einsum(eq, a, b)
+        torch.cuda.synchronize()
+        reload = time.perf_counter() - t
+        for _ in range(20):
+            einsum(eq, a, b)
+        torch.cuda.synchronize()
+        n = 200
+        t = time.perf_counter()
+        for _ in range(n):
+            einsum(eq, a, b)
+        host = (time.perf_counter() - t) / n
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(n):
+            einsum(eq, a, b)
+        e1.record()
+        torch.cuda.synchronize()
+        loop = e0.elapsed_time(e1) / n
+    finally:
+        if old is None:
+            os.environ.pop("EINSUM_BUILD_DIR", None)
+        else:
+            os.environ["EINSUM_BUILD_DIR"] = old
+        pb.clear_runner_cache()
+        shutil.rmtree(tmp, ignore_errors=True)
+    row = dict(equation=f"{eq} float32 (256, 257) x (257, 255)", first_call_ms=round(first * 1e3, 2),
+               reload_call_ms=round(reload * 1e3, 2), cached_call_host_us=round(host * 1e6, 1),
+               cached_call_loop_us=round(loop * 1e3, 1))
+    log(f"bench: einsum() first call {first * 1e3:.1f} ms (plan + compile + load), after a runner-cache clear "
+        f"{reload * 1e3:.1f} ms, cached call {host * 1e6:.1f} us host, {loop * 1e3:.1f} us per call back to back")
+    return row
+
+
+def launch_floor(dev, config1_row):
+    """Per-launch time of the launch probe (one wave storing one float)
+    replayed in a graph with as many launches as config 1's rotation, the
+    floor config 1's 256^3 GEMM is read against."""
+    import torch
+
+    from pto_einsum import abi
+
+    lib = abi.bind()
+    nsets = config1_row["sets"] if config1_row else 1024
+    bufs = [(torch.empty(64, dtype=torch.float32, device=dev),) for _ in range(nsets)]
+
+    def call(buf):
+        rc = lib.pe_probe_launch(ctypes.c_void_p(buf.data_ptr()), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        if rc != 0:
+            raise RuntimeError("launch probe failed")
+
+    ms = time_graph(call, bufs)
+    row = dict(kernel="launch probe (one wave, one store)", us=round(ms * 1e3, 2), launches_per_replay=nsets)
+    if config1_row:
+        row["config1_us"] = config1_row["us"]
+        row["config1_over_floor_us"] = round(config1_row["us"] - ms * 1e3, 2)
+    log(f"bench: launch floor {ms * 1e3:.2f} us per launch in a graph of {nsets}")
+    return row
 
 
 # -------------------------------------------------------------------- main --
@@ -829,7 +1038,7 @@ def main():
     call, operands, set_bytes = head.prepare(dev)
     nsets = n_sets(set_bytes)
     sets = replicate(operands, nsets)
-    a, b = operands
+    a, b = operands[:2]
     eq = "bji,bjk->bik"
     log(f"bench: config 2 {eq} {tuple(a.shape)} x {tuple(b.shape)} float32, {nsets} rotated operand sets")
     per, total_ms = time_runner(call, sets, args.steps, args.warmup)
@@ -858,12 +1067,16 @@ def main():
         rows["large_f16"] += time_torch_matmul(dev)
         rows["vendor_thin"] = time_torch_thin(dev)
         rows["gdn_stages"] = time_gdn_stages(dev, args.steps)
+        rows["launch_floor"] = launch_floor(dev, next((r for r in pc if r["config"] == "1"), None))
+        rows["cold_call"] = cold_call(dev)
 
     cpu = None
     if not args.no_cpu:
         log("bench: timing the CPU baseline")
         cpu = cpu_baseline(args.cpu_seconds)
         log(f"bench: cpu baseline {cpu}")
+        if not args.no_configs:
+            cpu_per_config(rows["per_config"], groups["per_config"])
 
     line = {
         "metric": "einsum TFLOP/s & HBM GB/s as % of MI355X roofline, per equation",

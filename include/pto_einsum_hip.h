@@ -119,9 +119,17 @@ typedef struct pe_einsum_plan {
 int pe_product(const pe_product_desc* d, const void* in0, const void* in1, float* out,
                void* stream);
 int pe_permute(const pe_permute_desc* d, const void* src, void* dst, void* stream);
+/* pe_gemm's workspace (0 when K is not split): the split-K partial sums,
+ * nsplit x batches x M x N float32, summed in split order by a second
+ * kernel. */
 int64_t pe_gemm_workspace_bytes(const pe_gemm_desc* d);
 int pe_gemm(const pe_gemm_desc* d, const void* a, const void* b, float* c, void* ws,
             int64_t ws_bytes, void* stream);
+/* The tile and K split the workspace query sizes for (no counterpart in the
+ * reference; for tests and tuning): info[0..3] = tile rows, tile columns,
+ * K splits, k per split.  Operand layouts can change the kernel but not the
+ * split. */
+int pe_gemm_choice(const pe_gemm_desc* d, int64_t* info);
 
 /* Fused linear-attention chain.  No single entry point of the reference
  * corresponds: it runs the chain as three einsums with float32 intermediates
@@ -195,7 +203,9 @@ int64_t pe_reduce_workspace_bytes(const pe_reduce_desc* d);
  * depends on src's 16-byte alignment), into order[0..2]. */
 int pe_reduce_order(const pe_reduce_desc* d, const void* src, int64_t* order);
 
-/* Plan executor: the body of every per-shape run_einsum_exec. */
+/* Plan executor: the body of every per-shape run_einsum_exec.  Every
+ * workspace region a plan uses is written before it is read, so a workspace
+ * needs no clearing between calls (or plans). */
 int pe_einsum_exec(const pe_einsum_plan* p, const void* in0, const void* in1, float* out,
                    void* ws, void* stream);
 /* Workspace bytes a plan needs (>= 256): what pe_einsum_setup allocates, for
@@ -237,6 +247,10 @@ const char* pe_version(void);
 int pe_probe_mfma(int dtype, int random, int64_t iters, float* out, int64_t out_len, void* stream);
 int64_t pe_probe_mfma_flops(int dtype, int64_t iters);
 int64_t pe_probe_out_len(void);
+/* Launch-floor probe (no counterpart in the reference): enqueues one wave that
+ * stores out[0] = 0, the least work a launch can carry; its time per launch
+ * in a graph replay is the fixed cost any kernel pays on the device. */
+int pe_probe_launch(float* out, void* stream);
 
 /* ---- per-shape entry points (one JIT library per equation/shapes/dtype) ----
  * Declared here with T = void; the generated source defines them with the

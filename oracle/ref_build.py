@@ -36,7 +36,7 @@ REF_INCLUDE = "/root/reference/src/pto_einsum/include"
 sys.path.insert(0, ORACLE_DIR)
 
 import oracle  # noqa: E402
-from ref_cases import REF_CASES  # noqa: E402
+from ref_cases import BENCH_CONFIG_CASES, REF_CASES  # noqa: E402
 
 
 def case_key(eq, shape0, shape1):
@@ -115,10 +115,12 @@ def build_case(eq, shape0, shape1):
     return so
 
 
-def build_all(jobs=8, cases=REF_CASES):
+def build_all(jobs=8, cases=None):
     if not available():
         print(f"ref_build: {REF_INCLUDE} not present; oracle/_ref not built")
         return []
+    if cases is None:
+        cases = list(dict.fromkeys(tuple(c) for c in REF_CASES + BENCH_CONFIG_CASES))
     os.makedirs(REF_DIR, exist_ok=True)
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         return list(ex.map(lambda c: build_case(*c), cases))

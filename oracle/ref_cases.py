@@ -14,7 +14,11 @@ exactly the routes the reference exercises:
 * ``CONFIG_CASES``     -- the benchmark equations at reduced sizes, plus edge
   shapes (size-1 axes, scalar output, multi-axis contraction order);
 * ``BENCH_SAMPLE``     -- the CPU baseline bench.py times: the whole of
-  config 2 (``bji,bjk->bik``, b=16, j=777, i=1000, k=1536).
+  config 2 (``bji,bjk->bik``, b=16, j=777, i=1000, k=1536);
+* ``BENCH_CONFIG_CASES`` -- every benchmark config at full size (config 2 is
+  ``BENCH_SAMPLE``), which bench.py times on the reference CPU route beside
+  each GPU row.  They are built but not run by the tests (config 3 alone is
+  68.7 G multiply-adds).
 """
 
 EINSUM_CASES = [
@@ -128,6 +132,18 @@ CONFIG_CASES = [
 ]
 
 BENCH_SAMPLE = ("bji,bjk->bik", (16, 777, 1000), (16, 777, 1536))
+
+BENCH_CONFIG_CASES = [
+    ("ij,jk->ik", (256, 256), (256, 256)),                          # 1
+    BENCH_SAMPLE,                                                   # 2
+    ("bshd,bthd->bsht", (4, 2048, 32, 128), (4, 2048, 32, 128)),    # 3
+    ("ts,ts->ts", (8192, 8192), (8192, 8192)),                      # 4a
+    ("bsd,d->bsd", (8, 4096, 4096), (4096,)),                       # 4b
+    ("tn,sn->ts", (4096, 128), (4096, 128)),                        # 5.1
+    ("ts,ts->ts", (4096, 4096), (4096, 4096)),                      # 5.2
+    ("ts,sp->tp", (4096, 4096), (4096, 128)),                       # 5.3
+    ("bshd,sd->bshd", (2, 4096, 32, 128), (4096, 128)),             # 5.R
+]
 
 REF_CASES = (EINSUM_CASES + ATTENTION_CASES + BROADCAST_CASES + CHAIN_CASES
              + CONFIG_CASES + [BENCH_SAMPLE])

@@ -511,6 +511,18 @@ int validate_gemm(const pe_gemm_desc& d) {
 
 }  // namespace pe
 
+extern "C" int pe_gemm_choice(const pe_gemm_desc* d, int64_t* info) {
+    if (!d || !info) return pe::fail(PE_ERR_INVALID, "gemm_choice: null argument");
+    const int st = pe::validate_gemm(*d);
+    if (st != PE_OK) return st;
+    const pe::GemmChoice c = pe::choose(*d);
+    info[0] = c.bm;
+    info[1] = c.bn;
+    info[2] = c.nsplit;
+    info[3] = c.k_per_split;
+    return PE_OK;
+}
+
 extern "C" int64_t pe_gemm_workspace_bytes(const pe_gemm_desc* d) {
     if (!d || pe::validate_gemm(*d) != PE_OK) return 0;
     if (d->K == 0 || d->M == 0 || d->N == 0 || pe::batch_total(*d) == 0) return 0;

@@ -77,8 +77,24 @@ __global__ __launch_bounds__(256, 2) void mfma_probe_kernel(int64_t iters, int32
     out[int64_t(blockIdx.x) * 256 + tid] = s;
 }
 
+// Launch-floor probe: one wave that stores one float.  Replayed in a graph
+// beside the small GEMMs, its time per launch is the fixed cost any kernel
+// pays on this device (dispatch, wave launch, completion signal), the floor
+// a launch-bound case such as a 256^3 GEMM is read against.
+__global__ __launch_bounds__(64) void launch_probe_kernel(float* out) {
+    if (threadIdx.x == 0) out[0] = 0.0f;
+}
+
 }  // namespace
 }  // namespace pe
+
+extern "C" int pe_probe_launch(float* out, void* stream) {
+    using namespace pe;
+    if (!out) return fail(PE_ERR_INVALID, "probe_launch: null output");
+    hipLaunchKernelGGL(launch_probe_kernel, dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream), out);
+    PE_CHECK_HIP(hipGetLastError());
+    return PE_OK;
+}
 
 extern "C" int64_t pe_probe_mfma_flops(int dtype, int64_t iters) {
     // blocks x 4 waves x iters x (2 * kChains) MFMAs x flops per MFMA

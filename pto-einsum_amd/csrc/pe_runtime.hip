@@ -68,7 +68,7 @@ extern "C" const char* pe_last_error(void) { return pe::g_last_error.c_str(); }
 
 extern "C" int pe_device_cu_count(void) { return pe::cu_count(); }
 
-extern "C" const char* pe_version(void) { return "pto-einsum-amd 0.1.0 (gfx950)"; }
+extern "C" const char* pe_version(void) { return "pto-einsum-amd 0.2.0 (gfx950)"; }
 
 extern "C" int64_t pe_einsum_workspace_bytes(const pe_einsum_plan* p) {
     return p ? pe::plan_workspace_bytes(*p) : 0;

@@ -24,4 +24,4 @@ from .graph import StageGraph
 from .linattn import linear_attention
 
 __all__ = ["einsum", "EinsumBuilder", "INCLUDE_DIR", "linear_attention", "StageGraph"]
-__version__ = "0.1.0"
+__version__ = "0.2.0"

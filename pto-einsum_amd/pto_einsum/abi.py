@@ -129,6 +129,7 @@ def bind(lib=None):
     lib.pe_gemm.argtypes = [ctypes.POINTER(GemmDesc), vp, vp, vp, vp, ctypes.c_int64, vp]
     lib.pe_gemm_workspace_bytes.argtypes = [ctypes.POINTER(GemmDesc)]
     lib.pe_gemm_workspace_bytes.restype = ctypes.c_int64
+    lib.pe_gemm_choice.argtypes = [ctypes.POINTER(GemmDesc), ctypes.POINTER(ctypes.c_int64)]
     lib.pe_einsum_exec.argtypes = [ctypes.POINTER(EinsumPlan), vp, vp, vp, vp, vp]
     lib.pe_einsum_workspace_bytes.argtypes = [ctypes.POINTER(EinsumPlan)]
     lib.pe_einsum_workspace_bytes.restype = ctypes.c_int64
@@ -148,7 +149,8 @@ def bind(lib=None):
     lib.pe_probe_mfma_flops.argtypes = [ctypes.c_int, ctypes.c_int64]
     lib.pe_probe_mfma_flops.restype = ctypes.c_int64
     lib.pe_probe_out_len.restype = ctypes.c_int64
-    for f in ("pe_product", "pe_permute", "pe_gemm", "pe_einsum_exec", "pe_einsum_teardown", "pe_einsum_run", "pe_probe_mfma",
+    lib.pe_probe_launch.argtypes = [vp, vp]
+    for f in ("pe_product", "pe_permute", "pe_gemm", "pe_einsum_exec", "pe_einsum_teardown", "pe_einsum_run", "pe_probe_mfma", "pe_probe_launch", "pe_gemm_choice",
               "pe_einsum_exec_noalloc", "pe_linear_attention", "pe_reduce_axes", "pe_reduce_order"):
         getattr(lib, f).restype = ctypes.c_int
     return lib

@@ -52,7 +52,7 @@ def _rows(t: torch.Tensor) -> torch.Tensor:
 
 
 def linear_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, m: torch.Tensor,
-                     *, split: int = 0, precise: bool = False) -> torch.Tensor:
+                     *, split: int = 0, precise: bool = False, out: torch.Tensor | None = None) -> torch.Tensor:
     """Fused ``einsum("tn,sn,sp,ts->tp", q, k, v, m)``; returns a float32
     [T, P] tensor on the operands' GPU.
 
@@ -60,7 +60,8 @@ def linear_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, m: torch
     float16, N <= 128 for float32); v [S, P] and m [T, S] are float16 or
     float32.  ``split`` forces the number of s splits (0 = choose);
     ``precise`` computes P.V on float32 matrix cores instead of the split
-    bfloat16 terms."""
+    bfloat16 terms.  ``out``: a contiguous float32 [T, P] tensor on the same
+    GPU to write into (else a new one is returned)."""
     for name, t in (("q", q), ("k", k), ("v", v), ("m", m)):
         if t.dim() != 2:
             raise ValueError(f"linear_attention: {name} must be 2-D, got shape {tuple(t.shape)}")
@@ -77,6 +78,9 @@ def linear_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, m: torch
     if dev.type != "cuda" or any(t.device != dev for t in (k, v, m)):
         raise ValueError("linear_attention: operands must all live on one GPU")
     q, k, v, m = (_rows(t) for t in (q, k, v, m))
+    if out is not None and (out.dtype != torch.float32 or tuple(out.shape) != (T, P) or out.device != dev
+                            or not out.is_contiguous()):
+        raise ValueError(f"linear_attention: out must be a contiguous float32 tensor of shape {(T, P)} on {dev}")
 
     d = abi.LinAttnDesc()
     d.qk_dtype, d.v_dtype, d.m_dtype, d.split = _DT[q.dtype], _DT[v.dtype], _DT[m.dtype], int(split)
@@ -86,7 +90,8 @@ def linear_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, m: torch
     d.q_numel, d.k_numel, d.v_numel, d.m_numel = (_extent(t) for t in (q, k, v, m))
     lib = abi.bind()
     with torch.cuda.device(dev):
-        out = torch.empty((T, P), dtype=torch.float32, device=dev)
+        if out is None:
+            out = torch.empty((T, P), dtype=torch.float32, device=dev)
         ws_bytes = lib.pe_linear_attention_workspace_bytes(ctypes.byref(d))
         ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
         rc = lib.pe_linear_attention(ctypes.byref(d), ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(k.data_ptr()),

@@ -1,6 +1,6 @@
-"""The GEMM tile / split choice, read on the CPU through pe_gemm_workspace_bytes
-(the workspace is nsplit x batches x M x N float32 partials, 0 when K is not
-split; with no GPU the library assumes MI355X's 256 CUs).  Pins the choices
+"""The GEMM tile / split choice, read on the CPU through pe_gemm_choice (the
+choice the workspace query sizes for; with no GPU the library assumes
+MI355X's 256 CUs), and the workspace size that follows from it.  Pins the choices
 the measured tuning made: the busiest-CU split counts of long-K grids, the
 rebalancing of part-filled rounds, and the grids that must keep their choice
 (the benchmark configurations)."""
@@ -16,9 +16,17 @@ def _splits(M, N, K, dtype="f32", nb=1):
     d = launch.GemmDesc(dtype=code, batch_shape=[nb], a_bstride=[M * K], b_bstride=[K * N], c_bstride=[M * N],
                         M=M, N=N, K=K, a_ms=K, a_ks=1, b_ks=N, b_ns=1, c_ms=N, c_ns=1,
                         a_numel=nb * M * K, b_numel=nb * K * N, c_numel=nb * M * N)
-    ws = int(abi.bind().pe_gemm_workspace_bytes(ctypes.byref(abi.gemm_desc(d))))
-    assert ws % (nb * M * N * 4) == 0
-    return ws // (nb * M * N * 4)
+    lib = abi.bind()
+    info = (ctypes.c_int64 * 4)()
+    assert lib.pe_gemm_choice(ctypes.byref(abi.gemm_desc(d)), info) == 0
+    bm, bn, split, kps = list(info)
+    ws = int(lib.pe_gemm_workspace_bytes(ctypes.byref(abi.gemm_desc(d))))
+    if split == 1:
+        assert ws == 0
+        return 0
+    assert ws == split * nb * M * N * 4     # the partials of every split
+    assert split == -(-K // kps)
+    return split
 
 
 @pytest.mark.parametrize("shape,dtype,want", [
