@@ -80,10 +80,19 @@ struct F16 {
     __device__ __forceinline__ static float to_f32(_Float16 x) { return (float)x; }
 };
 
-// Outputs at least this large are written with non-temporal stores; smaller
-// ones (which the 256 MB Infinity Cache holds) with ordinary stores.
+// Outputs at least this large are written with non-temporal stores, smaller
+// ones with ordinary stores.  Measured with a fresh output buffer per call
+// (the outputs rotating over 1 GiB, as a caller's successive results do):
+// 32 MB against the earlier 128 MB took config 5.1's 67 MB GEMM output from
+// 19.5 to 17.7 us and the GDN 64x16 / 16x48 products (67 / 50 MB) 4 % lower;
+// 8 MB changed nothing further.  Split-K partials, which the reduction
+// kernel reads back at once, keep ordinary stores up to
+// PE_NT_PARTIAL_MIN_BYTES.
 #ifndef PE_NT_MIN_BYTES
-#define PE_NT_MIN_BYTES (128ll << 20)
+#define PE_NT_MIN_BYTES (32ll << 20)
+#endif
+#ifndef PE_NT_PARTIAL_MIN_BYTES
+#define PE_NT_PARTIAL_MIN_BYTES (128ll << 20)
 #endif
 
 // Non-temporal vector stores (global_store_* ... nt), written as inline

@@ -42,6 +42,21 @@
 #ifndef PE_GEMM_KS_MAX_K
 #define PE_GEMM_KS_MAX_K 1024
 #endif
+// Unsplit float32 grids of at most this many 64x64 tiles per CU, with K of at
+// least PE_GEMM_KS_MIN_K, take the k-split kernel too; its 64x64 instantiation
+// serves grids of at most PE_GEMM_KS_TILE64_PER_CU such tiles per CU (else
+// 32x32 tiles).  Widening the rule to the GDN chunk products (256 x 128^3,
+// K = 128, four 64x64 tiles per CU) measured 30-32 us against 20 us on the
+// direct-load kernel's 64x64 tiles.
+#ifndef PE_GEMM_KS_TILES_PER_CU
+#define PE_GEMM_KS_TILES_PER_CU 2
+#endif
+#ifndef PE_GEMM_KS_MIN_K
+#define PE_GEMM_KS_MIN_K 256
+#endif
+#ifndef PE_GEMM_KS_TILE64_PER_CU
+#define PE_GEMM_KS_TILE64_PER_CU 1
+#endif
 
 // float16 GEMMs bound by matrix-core issue take 256x256 tiles (pe_gemm_big.h)
 // when those fill at least one round of CUs.
@@ -630,10 +645,11 @@ extern "C" int pe_gemm(const pe_gemm_desc* d, const void* a, const void* b, floa
     const int64_t cus = cu_count();
     const int64_t tiles64 = nb * ceil_div(d->M, 64) * ceil_div(d->N, 64);
     const int64_t tiles32 = nb * ceil_div(d->M, 32) * ceil_div(d->N, 32);
-    int ks_tile = (4 * tiles64 >= 3 * cus && tiles64 <= cus) ? 64 : 32;
+    int ks_tile = (4 * tiles64 >= 3 * cus && tiles64 <= PE_GEMM_KS_TILE64_PER_CU * cus) ? 64 : 32;
     bool ks_k;
     if (d->dtype == PE_F32) {
-        ks_k = d->K <= PE_GEMM_KS_MAX_K ? (ch.nsplit > 1 || (tiles64 <= 2 * cus && d->K >= 256))
+        ks_k = d->K <= PE_GEMM_KS_MAX_K ? (ch.nsplit > 1 || (tiles64 <= PE_GEMM_KS_TILES_PER_CU * cus &&
+                                                             d->K >= PE_GEMM_KS_MIN_K))
                                         : (d->K <= 2 * PE_GEMM_KS_MAX_K && ch.nsplit > 1 && tiles32 >= cus);
     } else {
         ks_tile = 64;
@@ -678,7 +694,7 @@ extern "C" int pe_gemm(const pe_gemm_desc* d, const void* a, const void* b, floa
     g.nbatch_total = uint32_t(nb);
     g.total_blocks = g.tiles_per_batch * g.nbatch_total * uint32_t(ch.nsplit);
     g.grid = g.total_blocks;
-    g.store_nt = (ch.nsplit > 1 ? ch.ws_bytes : nb * d->M * d->N * 4) >= PE_NT_MIN_BYTES;
+    g.store_nt = ch.nsplit > 1 ? ch.ws_bytes >= PE_NT_PARTIAL_MIN_BYTES : nb * d->M * d->N * 4 >= PE_NT_MIN_BYTES;
     g.a_ms = d->a_ms; g.a_ks = d->a_ks; g.b_ks = d->b_ks; g.b_ns = d->b_ns;
     g.c_ms = d->c_ms; g.c_ns = d->c_ns;
     g.nbatch = d->nbatch;
