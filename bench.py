@@ -768,10 +768,12 @@ def time_torch_matmul(dev):
 
 
 def time_torch_thin(dev, calls=50):
-    """torch.matmul (hipBLASLt) on config 5's two thin contractions, with the
-    operand rotation of the per-config rows: 5.1 tn,sn->ts in float16 (float16
-    output, half the bytes this path's float32 output writes) and 5.3
-    ts,sp->tp in float32 with TF32 off (this path's precision)."""
+    """The vendor library (torch.matmul / torch.bmm -> hipBLASLt) on config 5's
+    two thin contractions and on the headline, with the operand rotation of
+    the per-config rows: 5.1 tn,sn->ts in float16 (float16 output, half the
+    bytes this path's float32 output writes), 5.3 ts,sp->tp and config 2
+    bji,bjk->bik (A read transposed, as here) in float32 with TF32 off (this
+    path's precision)."""
     import torch
 
     g = torch.Generator().manual_seed(51)
@@ -780,7 +782,11 @@ def time_torch_thin(dev, calls=50):
               (torch.randn(4096, 128, generator=g) * 128 ** -0.5).to(f16), lambda a, b: torch.matmul(a, b.t()),
               4096 * 4096 * 2),
              ("5.3", "ts,sp->tp", torch.rand(4096, 4096, generator=g), torch.randn(4096, 128, generator=g),
-              torch.matmul, 4096 * 128 * 4))
+              torch.matmul, 4096 * 128 * 4),
+             # the headline contraction in its own layout: A read transposed
+             # (a [b, j, i] view as [b, i, j]), float32 in and out
+             ("2", "bji,bjk->bik", torch.randn(16, 777, 1000, generator=g), torch.randn(16, 777, 1536, generator=g),
+              lambda a, b: torch.bmm(a.transpose(1, 2), b), 16 * 1000 * 1536 * 4))
     tf32 = torch.backends.cuda.matmul.allow_tf32
     torch.backends.cuda.matmul.allow_tf32 = False
     out = []
@@ -798,8 +804,9 @@ def time_torch_thin(dev, calls=50):
             e1.record()
             torch.cuda.synchronize()
             t = e0.elapsed_time(e1) / calls
-            out.append(dict(config=cfg, equation=f"torch.matmul {eq} ({a.dtype} in and out)", us=round(t * 1e3, 2),
-                            operand_sets=len(sets)))
+            tf = (2 * 16 * 1000 * 1536 * 777 if cfg == "2" else 2 * 4096 * 4096 * 128) / (t * 1e-3) / 1e12
+            out.append(dict(config=cfg, equation=f"torch.{'bmm' if cfg == '2' else 'matmul'} {eq} ({a.dtype} in and out)",
+                            us=round(t * 1e3, 2), tflops=round(tf, 2), operand_sets=len(sets)))
             log(f"bench: torch.matmul {cfg} {eq} {t * 1e3:.1f} us")
             del sets, a, b
     finally:

@@ -58,6 +58,21 @@
 #define PE_GEMM_KS_TILE64_PER_CU 1
 #endif
 
+// float16 products with K in (96, 128] take the short-K kernel (all of K
+// resident in LDS) on grids of at most this many 128x128 tiles per CU.
+// Measured on MI355X against the two-stage direct-load kernel (float32
+// output, cold operands and outputs): 4096^2 x 128 (config 5.1, 4 tiles per
+// CU) 18.0 -> 16.2 us, 4096 x 8192 x 128 (8) 31.0 -> 26.9, 8192^2 x 128 (16)
+// 51.6 -> 48.2, 8192 x 16384 x 128 (32) 117.9 -> 92.8; config 3 (128 tiles
+// per CU, its 2.15 GB output the bound) 403-412 -> 439 us, so it keeps the
+// two-stage kernel, whose four blocks per CU keep more stores in flight.
+#ifndef PE_GEMM_RES
+#define PE_GEMM_RES 1
+#endif
+#ifndef PE_GEMM_RES_MAX_TILES_PER_CU
+#define PE_GEMM_RES_MAX_TILES_PER_CU 32
+#endif
+
 // float16 GEMMs bound by matrix-core issue take 256x256 tiles (pe_gemm_big.h)
 // when those fill at least one round of CUs.
 #ifndef PE_GEMM_BIG_F16
@@ -250,6 +265,12 @@ GemmChoice choose(const pe_gemm_desc& d, bool dl = false, int al = L_MN, int bl 
     const int bk = gemm_bk(d.dtype);
     const int64_t cus = cu_count();
     c.persist = PE_GEMM_PERSIST;
+    if (d.tile == 2) {  // the short-K kernel: 128x128 tiles, all of K in one block
+        c.bm = c.bn = 128;
+        c.nsplit = 1;
+        c.k_per_split = int(d.K);
+        return c;
+    }
     if (d.tile == 64 || d.tile == 128) {
         c.bm = c.bn = d.tile;
     } else if (d.tile == 192 || d.tile == 256) {
@@ -467,6 +488,34 @@ GemmChoice choose(const pe_gemm_desc& d, bool dl = false, int al = L_MN, int bl 
     return c;
 }
 
+// Launch of the short-K kernel (gemm_res_kernel) for descriptor d.
+hipError_t launch_res(const pe_gemm_desc& d, const void* a, const void* b, float* c, int64_t nb, int al, int bl,
+                      hipStream_t s) {
+    GemmArgs g{};
+    g.a = a; g.b = b; g.c = c;
+    g.partial = nullptr;
+    g.M = int32_t(d.M); g.N = int32_t(d.N); g.K = int32_t(d.K);
+    g.nsplit = 1;
+    g.k_per_split = int32_t(d.K);
+    g.tiles_m = int32_t(ceil_div(d.M, 128));
+    g.tiles_n = int32_t(ceil_div(d.N, 128));
+    g.tiles_per_batch = uint32_t(g.tiles_m) * uint32_t(g.tiles_n);
+    g.nbatch_total = uint32_t(nb);
+    g.total_blocks = g.tiles_per_batch * g.nbatch_total;
+    g.grid = g.total_blocks;
+    g.store_nt = nb * d.M * d.N * 4 >= PE_NT_MIN_BYTES;
+    g.a_ms = d.a_ms; g.a_ks = d.a_ks; g.b_ks = d.b_ks; g.b_ns = d.b_ns;
+    g.c_ms = d.c_ms; g.c_ns = d.c_ns;
+    g.nbatch = d.nbatch;
+    for (int i = 0; i < d.nbatch; ++i) {
+        g.batch_div[i].init(uint32_t(d.batch_shape[i]));
+        g.a_bs[i] = d.a_bstride[i];
+        g.b_bs[i] = d.b_bstride[i];
+        g.c_bs[i] = d.c_bstride[i];
+    }
+    return launch_gemm_res(al, bl, g, s);
+}
+
 int classify(int64_t rows, int64_t k, int64_t rs, int64_t ks, const int64_t* bs, int nb,
              const void* p, int vec) {
     // Extent-1 axes carry no stride; treat them as absent.
@@ -486,8 +535,10 @@ int validate_gemm(const pe_gemm_desc& d) {
     if (d.dtype != PE_F32 && d.dtype != PE_F16)
         return fail(PE_ERR_UNSUPPORTED, "gemm: dtype must be PE_F32 or PE_F16");
     if (d.nbatch < 0 || d.nbatch > PE_MAX_DIMS) return fail(PE_ERR_INVALID, "gemm: nbatch out of range");
-    if (d.tile != 0 && d.tile != 1 && d.tile != 64 && d.tile != 128 && d.tile != 192 && d.tile != 256)
-        return fail(PE_ERR_INVALID, "gemm: tile must be 0, 1, 64, 128, 192 or 256");
+    if (d.tile != 0 && d.tile != 1 && d.tile != 2 && d.tile != 64 && d.tile != 128 && d.tile != 192 && d.tile != 256)
+        return fail(PE_ERR_INVALID, "gemm: tile must be 0, 1, 2, 64, 128, 192 or 256");
+    if (d.tile == 2 && (d.dtype != PE_F16 || d.split_k > 1 || d.K <= 96 || d.K > 128))
+        return fail(PE_ERR_UNSUPPORTED, "gemm: the short-K kernel (tile 2) is float16 only, K in (96, 128], no split");
     if (d.tile == 1 && (d.dtype != PE_F16 || d.split_k > 1))
         return fail(PE_ERR_UNSUPPORTED, "gemm: the 256x256 tile (1) is float16 only, without a K split");
     if (d.tile == 192 && d.dtype != PE_F32)
@@ -606,6 +657,12 @@ extern "C" int pe_gemm(const pe_gemm_desc* d, const void* a, const void* b, floa
     if (d->tile == 1)
         return fail(PE_ERR_UNSUPPORTED,
                     "gemm: the 256x256 tile needs 16-byte vector operands and batch axes that merge into one");
+    if (d->tile == 2) {
+        if (!dl || gemm_res_resident(al, bl) < 1)
+            return fail(PE_ERR_UNSUPPORTED, "gemm: the short-K kernel (tile 2) needs 16-byte vector operands");
+        PE_CHECK_HIP(launch_res(*d, a, b, c, nb, al, bl, s));
+        return PE_OK;
+    }
     GemmChoice ch = choose(*d, dl, al, bl);
     if (dl && gemm_dl_resident(d->dtype, ch.bm, ch.bn, ch.minb, al, bl) < 1) {
         // the chosen direct-load instantiation spills: the staged kernel
@@ -643,6 +700,15 @@ extern "C" int pe_gemm(const pe_gemm_desc* d, const void* a, const void* b, floa
     // 4096 22.6 against 26.4, 1664 x 2304 x 3072 with 3.7 tiles per CU 48.8
     // against 60.1).
     const int64_t cus = cu_count();
+    // float16 products with K in (96, 128] (four 32-k slabs), unsplit, on
+    // 128x128 tiles: the short-K kernel, all of K in flight at once.
+    if (PE_GEMM_RES && dl && d->dtype == PE_F16 && d->split_k == 0 && d->tile == 0 && ch.nsplit == 1 &&
+        ch.bm == 128 && ch.bn == 128 && d->K > 96 && d->K <= 128 &&
+        nb * ceil_div(d->M, 128) * ceil_div(d->N, 128) <= PE_GEMM_RES_MAX_TILES_PER_CU * cus &&
+        gemm_res_resident(al, bl) >= 1) {
+        PE_CHECK_HIP(launch_res(*d, a, b, c, nb, al, bl, s));
+        return PE_OK;
+    }
     const int64_t tiles64 = nb * ceil_div(d->M, 64) * ceil_div(d->N, 64);
     const int64_t tiles32 = nb * ceil_div(d->M, 32) * ceil_div(d->N, 32);
     int ks_tile = (4 * tiles64 >= 3 * cus && tiles64 <= PE_GEMM_KS_TILE64_PER_CU * cus) ? 64 : 32;

@@ -512,4 +512,140 @@ __global__ __launch_bounds__(kGemmThreads, MINB) void gemm_dl_kernel(GemmArgs g)
     }
 }
 
+// Short-K variant: every k slab of the tile resident in LDS at once.  One
+// block per output tile (no split, no persistent walk); each wave issues the
+// loads of all NS slabs into NS LDS stages up front and then computes slab by
+// slab, waiting only until its own loads of that slab have landed (vmcnt
+// counts the later slabs' loads still in flight) and for the other waves'
+// (one barrier per slab).  For K in ((NS - 1) BK, NS BK]: the two-stage ring
+// of gemm_dl_kernel keeps one slab of loads ahead of the MFMAs, and where a
+// slab's MFMAs take far less than a load's latency (float16, 128 x 128
+// tiles: 8 MFMAs of 32 cycles per wave and slab) its NS slabs cost NS load
+// latencies in a row; here they cost one.  LDS: NS x (BM + BN) x 64 bytes
+// (64 KB for 128 x 128 float16 tiles and K = 128, two blocks per CU).
+// Measured on MI355X: config 5.1 (tn,sn->ts, 4096^2 x 128 float16, float32
+// out) with its output stores removed ran 9.5 us of its 17.8; float32 short K
+// (the GDN chunk products, K = 128 in eight slabs at one block per CU) ran
+// slower than the two-stage kernel (22 against 20 us at 256 x 128^3, 68
+// against 54 us at 1024 x 128^3): its MFMAs per slab outlast a load, and one
+// wave per SIMD issues them less densely than four.
+template <typename E, int BM, int BN, int AL, int BL, int NS, int MINB>
+__global__ __launch_bounds__(kGemmThreads, MINB) void gemm_res_kernel(GemmArgs g) {
+    using T = typename E::T;
+    using M = DlMath<E>;
+    using OA = DlOperand<E, BM, AL, true>;
+    using OB = DlOperand<E, BN, BL, true>;
+    constexpr int BK = M::BK;
+    constexpr int WM = BM / 2, WN = BN / 2;
+    constexpr int FM = WM / 32, FN = WN / 32;
+    constexpr int PER_SLAB = OA::NI + OB::NI;  // load instructions per wave per slab
+    static_assert((NS - 1) * PER_SLAB <= 63, "vmcnt counts at most 63 loads");
+    __shared__ __attribute__((aligned(16))) T sa[NS][OA::ELEMS];
+    __shared__ __attribute__((aligned(16))) T sb[NS][OB::ELEMS];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+
+    uint32_t t = blockIdx.x;
+    const uint32_t batch = t / g.tiles_per_batch;
+    t -= batch * g.tiles_per_batch;
+    const int tm = int(t / uint32_t(g.tiles_n));
+    const int tn = int(t - uint32_t(tm) * uint32_t(g.tiles_n));
+    int64_t a_off = 0, b_off = 0, c_off = 0;
+    uint32_t rem = batch;
+    for (int d = g.nbatch - 1; d >= 0; --d) {
+        uint32_t q, r;
+        g.batch_div[d].divmod(rem, q, r);
+        a_off += int64_t(r) * g.a_bs[d];
+        b_off += int64_t(r) * g.b_bs[d];
+        c_off += int64_t(r) * g.c_bs[d];
+        rem = q;
+    }
+    const int m0 = tm * BM, n0 = tn * BN;
+    const T* A = static_cast<const T*>(g.a) + a_off + int64_t(m0) * g.a_ms;
+    const T* B = static_cast<const T*>(g.b) + b_off + int64_t(n0) * g.b_ns;
+    const int rows_a = g.M - m0, rows_b = g.N - n0;
+
+    // Every slab's loads, in slab order (loads complete in issue order, so
+    // vmcnt(n) means all but this wave's last n loads have landed).
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+        const int kl = g.K - s * BK;
+        OA::load(A + int64_t(s) * BK * g.a_ks, g.a_ms, g.a_ks, rows_a, kl, sa[s], lane, wave);
+        OB::load(B + int64_t(s) * BK * g.b_ks, g.b_ns, g.b_ks, rows_b, kl, sb[s], lane, wave);
+    }
+
+    const typename OA::LaneOff loa = OA::lane_off(lane, wm * WM);
+    const typename OB::LaneOff lob = OB::lane_off(lane, wn * WN);
+    f32x16 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+        // This wave's loads of slab s have landed (those of the later slabs
+        // may still be in flight); after the barrier, every wave's have.
+        switch (NS - 1 - s) {
+#define PE_RES_WAIT(n) \
+    case n: asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" : : "n"((n) * PER_SLAB) : "memory"); break;
+            PE_RES_WAIT(0) PE_RES_WAIT(1) PE_RES_WAIT(2) PE_RES_WAIT(3)
+            PE_RES_WAIT(4) PE_RES_WAIT(5) PE_RES_WAIT(6) PE_RES_WAIT(7)
+#undef PE_RES_WAIT
+        }
+        const int k_left = g.K - s * BK;
+        if (k_left < BK) {
+            OA::zero_tail(sa[s], k_left, tid);
+            OB::zero_tail(sb[s], k_left, tid);
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        }
+        typename M::Frag fa[FM][OA::RING], fb[FN][OB::RING];
+        __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+        for (int i = 0; i < FM; ++i) OA::frag(sa[s], loa, wm * WM, i, 0, fa[i]);
+#pragma unroll
+        for (int j = 0; j < FN; ++j) OB::frag(sb[s], lob, wn * WN, j, 0, fb[j]);
+#pragma unroll
+        for (int st = 0; st < M::STEPS; ++st) {
+            if (st + 1 < M::STEPS) {
+#pragma unroll
+                for (int i = 0; i < FM; ++i) OA::frag(sa[s], loa, wm * WM, i, st + 1, fa[i]);
+#pragma unroll
+                for (int j = 0; j < FN; ++j) OB::frag(sb[s], lob, wn * WN, j, st + 1, fb[j]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    acc[i][j] = M::mfma(fa[i][st % OA::RING], fb[j][st % OB::RING], acc[i][j]);
+        }
+        __builtin_amdgcn_s_setprio(0);
+    }
+
+    // Epilogue, as gemm_dl_kernel's (no split).
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7");
+    const int wm0 = m0 + wm * WM, wn0 = n0 + wn * WN;
+    const float* wbase = dl_uniform_base(g.c + c_off + int64_t(wm0) * g.c_ms + int64_t(wn0) * g.c_ns);
+    uint32_t cms4 = uint32_t(g.c_ms) * 4u, cns4 = uint32_t(g.c_ns) * 4u, ln = uint32_t(lane);
+    int rrem = g.M - wm0, crem = g.N - wn0;
+    asm volatile("" : "+s"(cms4), "+s"(cns4), "+v"(ln), "+s"(rrem), "+s"(crem));
+    const uint32_t lo = (ln >> 5) * 4u * cms4 + (ln & 31u) * cns4;
+    const bool nt = g.store_nt != 0;
+    if (m0 + BM <= g.M && n0 + BN <= g.N) {
+        if (nt) dl_store_tile<true, false>(wbase, lo, cms4, cns4, 0, 0, acc);
+        else dl_store_tile<false, false>(wbase, lo, cms4, cns4, 0, 0, acc);
+    } else {
+        const int rr = rrem - 4 * int(ln >> 5), cr = crem - int(ln & 31u);
+        if (nt) dl_store_tile<true, true>(wbase, lo, cms4, cns4, rr, cr, acc);
+        else dl_store_tile<false, true>(wbase, lo, cms4, cns4, rr, cr, acc);
+    }
+}
+
 }  // namespace pe

@@ -1,0 +1,78 @@
+"""The short-K GEMM kernel (float16, K in (96, 128]: every k slab of a 128x128
+tile resident in LDS, all loads issued up front; forced with
+pe_gemm_desc.tile = 2 at sizes the automatic choice sends elsewhere): every
+operand layout pairing, K tails inside the last slab, partial tiles in M and
+N and batches, against a float64 reference, with run-to-run equality (the
+reference checks its batched matmul the same way, test_einsum.py:244-364);
+and config 5.1 and config-3-shaped products through the public einsum, which
+choose it."""
+import ctypes
+
+import pytest
+import torch
+
+from pto_einsum import abi, einsum, launch, runtime
+
+pytestmark = pytest.mark.gpu
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _check(got, A, B, rtol=2e-3):
+    want = torch.bmm(A.double(), B.double())
+    bound = torch.bmm(A.double().abs(), B.double().abs())
+    assert bool(((got.cpu().double() - want).abs() <= 1e-5 * bound + 1e-6).all())
+
+
+def test_refused_outside_its_range():
+    lib = abi.bind()
+    d = launch.GemmDesc(dtype=launch.DT_F16, batch_shape=[1], a_bstride=[0], b_bstride=[0], c_bstride=[0],
+                        M=128, N=128, K=64, a_ms=64, a_ks=1, b_ks=128, b_ns=1, c_ms=128, c_ns=1,
+                        a_numel=128 * 64, b_numel=64 * 128, c_numel=128 * 128, tile=2)
+    assert lib.pe_gemm(ctypes.byref(abi.gemm_desc(d)), None, None, None, None, 0, None) == -3
+    d.dtype, d.K = launch.DT_F32, 128
+    assert lib.pe_gemm(ctypes.byref(abi.gemm_desc(d)), None, None, None, None, 0, None) == -3
+
+
+@pytest.mark.parametrize("al,bl", [("mn", "mn"), ("mn", "k"), ("k", "mn"), ("k", "k")])
+@pytest.mark.parametrize("nb,M,N,K", [(3, 128, 128, 128), (2, 200, 136, 120), (5, 136, 264, 104),
+                                      (1, 1000, 384, 128), (4, 136, 72, 112)])
+def test_short_k_kernel_against_float64(al, bl, nb, M, N, K):
+    g = torch.Generator().manual_seed(nb * 1000 + M + N + K)
+    A = (torch.randn(nb, M, K, generator=g) / 8).half()
+    B = (torch.randn(nb, K, N, generator=g) / 8).half()
+    a_buf, a_ms, a_ks = (A.transpose(1, 2).contiguous(), 1, M) if al == "mn" else (A.contiguous(), K, 1)
+    b_buf, b_ks, b_ns = (B.contiguous(), N, 1) if bl == "mn" else (B.transpose(1, 2).contiguous(), 1, K)
+    d = launch.GemmDesc(dtype=launch.DT_F16, batch_shape=[nb], a_bstride=[M * K], b_bstride=[K * N],
+                        c_bstride=[M * N], M=M, N=N, K=K, a_ms=a_ms, a_ks=a_ks, b_ks=b_ks, b_ns=b_ns,
+                        c_ms=N, c_ns=1, a_numel=nb * M * K, b_numel=nb * K * N, c_numel=nb * M * N, tile=2)
+    lib = abi.bind()
+    cd = abi.gemm_desc(d)
+    assert lib.pe_gemm_workspace_bytes(ctypes.byref(cd)) == 0
+    a, b = a_buf.reshape(-1).cuda(), b_buf.reshape(-1).cuda()
+    outs = []
+    for _ in range(3):
+        c = torch.full((nb, M, N), float("nan"), device="cuda")
+        rc = lib.pe_gemm(ctypes.byref(cd), _ptr(a), _ptr(b), _ptr(c), None, 0,
+                         ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        assert rc == 0, runtime.last_error()
+        outs.append(c)
+    torch.cuda.synchronize()
+    _check(outs[0], A, B)
+    assert all(torch.equal(outs[0], o) for o in outs[1:])
+
+
+@pytest.mark.parametrize("eq,s0,s1", [("tn,sn->ts", (4096, 128), (4096, 128)),
+                                      ("bshd,bthd->bsht", (2, 512, 8, 128), (2, 384, 8, 128))])
+def test_public_einsum_shapes_that_take_it(eq, s0, s1):
+    """Config 5.1 itself and a config-3-shaped product (two batch axes, the
+    fused permuted store) through einsum(), against a float64 reference."""
+    g = torch.Generator().manual_seed(51)
+    x = (torch.randn(s0, generator=g) / 8).half()
+    y = (torch.randn(s1, generator=g) / 8).half()
+    got = einsum(eq, x.cuda(), y.cuda()).cpu().double()
+    want = torch.einsum(eq, x.double(), y.double())
+    bound = torch.einsum(eq, x.double().abs(), y.double().abs())
+    assert bool(((got - want).abs() <= 1e-5 * bound + 1e-6).all())
