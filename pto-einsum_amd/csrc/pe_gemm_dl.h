@@ -525,10 +525,13 @@ __global__ __launch_bounds__(kGemmThreads, MINB) void gemm_dl_kernel(GemmArgs g)
 // (64 KB for 128 x 128 float16 tiles and K = 128, two blocks per CU).
 // Measured on MI355X: config 5.1 (tn,sn->ts, 4096^2 x 128 float16, float32
 // out) with its output stores removed ran 9.5 us of its 17.8; float32 short K
-// (the GDN chunk products, K = 128 in eight slabs at one block per CU) ran
-// slower than the two-stage kernel (22 against 20 us at 256 x 128^3, 68
-// against 54 us at 1024 x 128^3): its MFMAs per slab outlast a load, and one
-// wave per SIMD issues them less densely than four.
+// (the GDN chunk products, K = 128 in eight slabs) ran slower than the
+// two-stage kernel both as 128 x 128 tiles at one block per CU (22 against
+// 20 us at 256 x 128^3, 68 against 54 us at 1024 x 128^3) and as 64 x 64
+// tiles at two per CU (21-22 against 19.5-21 us at 256 x 128^3): float32
+// MFMAs per slab take about as long as a load, so the two-stage ring at four
+// blocks per CU already hides the latency, and fewer resident waves issue
+// them less densely.
 template <typename E, int BM, int BN, int AL, int BL, int NS, int MINB>
 __global__ __launch_bounds__(kGemmThreads, MINB) void gemm_res_kernel(GemmArgs g) {
     using T = typename E::T;
