@@ -64,6 +64,7 @@ struct GemmArgs {
     uint32_t total_blocks;    // tiles_per_batch * nbatch_total * nsplit
     uint32_t grid;            // launched blocks (persistent when < total_blocks)
     int32_t store_nt;         // non-temporal stores for the output
+    int32_t off32;            // direct-load kernel: full slabs load from 32-bit per-lane offsets
     int64_t a_ms, a_ks, b_ks, b_ns, c_ms, c_ns;
     int32_t nbatch;
     FastDiv batch_div[PE_MAX_DIMS];

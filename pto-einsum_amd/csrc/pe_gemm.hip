@@ -770,6 +770,14 @@ extern "C" int pe_gemm(const pe_gemm_desc* d, const void* a, const void* b, floa
         g.b_bs[i] = d->b_bstride[i];
         g.c_bs[i] = d->c_bstride[i];
     }
+    // Direct-load full slabs address each operand vector by a 32-bit byte
+    // offset from the slab's base: (256 rows, BK k) of every operand within
+    // 2^32 bytes.
+    const int64_t elem = d->dtype == PE_F32 ? 4 : 2;
+    auto span_ok = [&](int64_t rs, int64_t ks) {  // a slab is 64 bytes of k
+        return rs >= 0 && ks >= 0 && (256 * rs + (64 / elem) * ks + 8) * elem < (int64_t(1) << 32);
+    };
+    g.off32 = dl && span_ok(d->a_ms, d->a_ks) && span_ok(d->b_ns, d->b_ks);
     hipError_t e = dl                   ? launch_gemm_dl(d->dtype, ch.bm, ch.bn, ch.minb, al, bl, !hbm_bound(*d), g, s)
                    : d->dtype == PE_F32 ? launch_gemm_f32(ch.bm, ch.bn, al, bl, ch.persist, g, s)
                                         : launch_gemm_f16(ch.bm, ch.bn, al, bl, PE_GEMM_F16_PERSIST, g, s);

@@ -113,18 +113,33 @@ __device__ __forceinline__ const float* dl_uniform_base(const float* p) {
     return b;
 }
 
+// LDS byte address of a pointer into a __shared__ array.  Taken once per
+// stage at kernel entry, where it folds to a constant: converted inside the
+// slab loop, the generic pointer is kept live and null-checked per load.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)(p)));
+}
+
 // 16 bytes per lane from global memory into LDS at lds + 16 * lane.  Written
 // as inline assembly so the compiler does not treat the in-flight load as a
 // pending write to every LDS array: it would otherwise wait for it before the
 // first read of the other stage, serialising loads and MFMAs.  Completion is
 // awaited explicitly (s_waitcnt vmcnt(0) before the barrier of the slab that
 // reads it).
-__device__ __forceinline__ void dma16(const float* gptr, const float* lds) {
+__device__ __forceinline__ void dma16(const float* gptr, uint32_t lds) {
     // The LDS address is wave-uniform (M0 takes a scalar register).
-    const uint32_t l = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(
-        reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) float*)(lds))));
+    const uint32_t l = __builtin_amdgcn_readfirstlane(lds);
     // One wait state between writing M0 and the load that reads it.
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(gptr), "s"(l) : "memory", "m0");
+}
+__device__ __forceinline__ void dma16(const float* gptr, const float* lds) { dma16(gptr, lds_addr(lds)); }
+
+// As dma16, from a wave-uniform 64-bit base (scalar registers) plus a
+// per-lane 32-bit byte offset: no per-lane 64-bit address arithmetic.
+__device__ __forceinline__ void dma16s(const void* sbase, uint32_t off, uint32_t lds) {
+    const uint32_t l = __builtin_amdgcn_readfirstlane(lds);
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+                 : : "v"(off), "s"(sbase), "s"(l) : "memory", "m0");
 }
 
 // Per-type slab geometry and MFMA.
@@ -184,11 +199,16 @@ struct DlOperand {
 
     // Issues the slab's loads into `stage`.  base: operand at (batch, tile
     // row 0, slab k 0); rows_left / k_left: valid extent from there.
+    // stage: LDS byte address.
     __device__ __forceinline__ static void load(const T* base, int64_t rs, int64_t ks, int rows_left,
-                                                int k_left, T* stage, int lane, int wave) {
+                                                int k_left, uint32_t stage, int lane, int wave) {
         static_assert(NI >= 1 && NCHUNK % 4 == 0, "every wave issues whole chunks");
 #pragma unroll
         for (int i = 0; i < NI; ++i) load_chunk(base, rs, ks, rows_left, k_left, stage, lane, i * 4 + wave);
+    }
+    __device__ __forceinline__ static void load(const T* base, int64_t rs, int64_t ks, int rows_left,
+                                                int k_left, T* stage, int lane, int wave) {
+        load(base, rs, ks, rows_left, k_left, lds_addr(stage), lane, wave);
     }
 
     // Row and k (relative to the stage's first row and k) that lane `lane`
@@ -208,11 +228,35 @@ struct DlOperand {
 
     // One wave's load of chunk c of a stage.
     __device__ __forceinline__ static void load_chunk(const T* base, int64_t rs, int64_t ks, int rows_left,
-                                                      int k_left, T* stage, int lane, int c) {
+                                                      int k_left, uint32_t stage, int lane, int c) {
         int r, k;
         chunk_rk(lane, c, rows_left, k_left, r, k);
-        dma16(reinterpret_cast<const float*>(base + int64_t(r) * rs + int64_t(k) * ks),
-              reinterpret_cast<const float*>(stage + c * (1024 / E::kBytes)));
+        dma16(reinterpret_cast<const float*>(base + int64_t(r) * rs + int64_t(k) * ks), stage + uint32_t(c) * 1024u);
+    }
+    __device__ __forceinline__ static void load_chunk(const T* base, int64_t rs, int64_t ks, int rows_left,
+                                                      int k_left, T* stage, int lane, int c) {
+        load_chunk(base, rs, ks, rows_left, k_left, lds_addr(stage), lane, c);
+    }
+
+    // Full-slab loads (every k of the slab in range; for L_K also every row of
+    // the tile) from one per-lane byte offset: this wave's chunk 4 i + wave
+    // sits at base + i * chunk_step + full_off.  L_MN: chunks differ only in
+    // k, by 4 KPC k rows (a multiple of 4, so the float16 swizzle and the row
+    // clamp are the same for all of them); L_K: by 64 rows.  Needs every
+    // offset below 2^32 bytes (GemmArgs::off32).
+    __device__ __forceinline__ static uint32_t full_off(int64_t rs, int64_t ks, int rows_left, int lane, int wave) {
+        int r, k;
+        chunk_rk(lane, wave, rows_left, BK, r, k);
+        return uint32_t((int64_t(r) * rs + int64_t(k) * ks) * E::kBytes);
+    }
+    __device__ __forceinline__ static int64_t chunk_step(int64_t rs, int64_t ks) {
+        return LAYOUT == L_MN ? int64_t(4 * KPC) * ks : int64_t(64) * rs;
+    }
+    __device__ __forceinline__ static bool full_ok(int rows_left) { return LAYOUT == L_MN || rows_left >= ROWS; }
+    __device__ __forceinline__ static void load_full(const T* base, int64_t step, uint32_t off, uint32_t stage,
+                                                     int wave) {
+#pragma unroll
+        for (int i = 0; i < NI; ++i) dma16s(base + i * step, off, stage + uint32_t(i * 4 + wave) * 1024u);
     }
 
     // Zeroes every k >= k_left of a stage (0 < k_left < BK).
@@ -389,16 +433,37 @@ __global__ __launch_bounds__(kGemmThreads, MINB) void gemm_dl_kernel(GemmArgs g)
     int ls = 0;              // its next slab to load
     bool lvalid = true;
 
-    auto issue = [&](T* da, T* db) {
+    // Per-lane byte offsets of the load tile's full slabs (computed once per
+    // tile; the slab's base advances in scalar registers).
+    uint32_t lofa = 0, lofb = 0;
+    auto set_lo = [&]() {
+        if (g.off32) {
+            lofa = OA::full_off(g.a_ms, g.a_ks, lt.rows_a, lane, wave);
+            lofb = OB::full_off(g.b_ns, g.b_ks, lt.rows_b, lane, wave);
+        }
+    };
+    set_lo();
+    const uint32_t la0 = lds_addr(sa0), la1 = lds_addr(sa1), lb0 = lds_addr(sb0), lb1 = lds_addr(sb1);
+    auto issue = [&](uint32_t da, uint32_t db) {
         const int kl = lt.k_len - ls * BK;
-        OA::load(lt.A + int64_t(ls) * BK * g.a_ks, g.a_ms, g.a_ks, lt.rows_a, kl, da, lane, wave);
-        OB::load(lt.B + int64_t(ls) * BK * g.b_ks, g.b_ns, g.b_ks, lt.rows_b, kl, db, lane, wave);
+        const T* pa = lt.A + int64_t(ls) * BK * g.a_ks;
+        const T* pb = lt.B + int64_t(ls) * BK * g.b_ks;
+        const bool full = g.off32 && kl >= BK;
+        if (full && OA::full_ok(lt.rows_a))
+            OA::load_full(pa, OA::chunk_step(g.a_ms, g.a_ks), lofa, da, wave);
+        else
+            OA::load(pa, g.a_ms, g.a_ks, lt.rows_a, kl, da, lane, wave);
+        if (full && OB::full_ok(lt.rows_b))
+            OB::load_full(pb, OB::chunk_step(g.b_ns, g.b_ks), lofb, db, wave);
+        else
+            OB::load(pb, g.b_ns, g.b_ks, lt.rows_b, kl, db, lane, wave);
         if (++ls == lt.nslabs) {
             lbid += walk.step;
             lvalid = lbid < walk.end;
             if (lvalid) {
                 lt = locate(lbid);
                 ls = 0;
+                set_lo();
             }
         }
     };
@@ -456,7 +521,7 @@ __global__ __launch_bounds__(kGemmThreads, MINB) void gemm_dl_kernel(GemmArgs g)
 
     // One slab: wait for its loads, start the next slab's loads into the
     // other stage, then the MFMAs.  Returns true when the block is done.
-    auto step = [&](const T* sa, const T* sb, T* na, T* nb) -> bool {
+    auto step = [&](const T* sa, const T* sb, uint32_t na, uint32_t nb) -> bool {
         // This wave's loads of the slab have landed; after the barrier every
         // wave's have, and every wave is done reading the other stage.
         asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
@@ -505,10 +570,10 @@ __global__ __launch_bounds__(kGemmThreads, MINB) void gemm_dl_kernel(GemmArgs g)
         return false;
     };
 
-    issue(sa0, sb0);
+    issue(la0, lb0);
     for (;;) {
-        if (step(sa0, sb0, sa1, sb1)) break;
-        if (step(sa1, sb1, sa0, sb0)) break;
+        if (step(sa0, sb0, la1, lb1)) break;
+        if (step(sa1, sb1, la0, lb0)) break;
     }
 }
 
