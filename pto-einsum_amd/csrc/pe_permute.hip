@@ -68,7 +68,11 @@ __device__ __forceinline__ void put(u32x4* p, const u32x4& v, bool nt) {
 }
 
 // Streamed gather: VEC elements of type W per vector (16 bytes when VEC > 1),
-// U vectors per lane in flight.
+// U vectors per lane in flight.  Every source vector is read once, with the
+// non-temporal hint (measured on MI355X: config 3 in0, 134 MB, 26.4-26.6 ->
+// 25.1-25.3 us; config 3's output permutation 715-718 -> 704-707 us; the
+// tiled transposes, whose neighbouring tiles share source lines, ran the
+// same or slower with it: config 2 in0 24.7-25.0 -> 27.8-28.0 us).
 template <typename W, int VEC, bool HAS_OUTER, int U>
 __global__ __launch_bounds__(kThreads) void gather_kernel(GatherArgs p) {
     const W* __restrict__ src = static_cast<const W*>(p.src);
@@ -97,7 +101,8 @@ __global__ __launch_bounds__(kThreads) void gather_kernel(GatherArgs p) {
             u32x4 x[U];
 #pragma unroll
             for (int u = 0; u < U; ++u)
-                if (v0 + u * stride < p.nvec) x[u] = *reinterpret_cast<const u32x4*>(src + off[u]);
+                if (v0 + u * stride < p.nvec)
+                    x[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + off[u]));
 #pragma unroll
             for (int u = 0; u < U; ++u)
                 if (v0 + u * stride < p.nvec)

@@ -70,6 +70,28 @@ struct ProductArgs {
 template <typename E, int VEC>
 struct VecLoad;
 
+// Vector load with the non-temporal hint (global_load ... nt), for the first
+// operand of a flat stream (one merged axis: every element read once).  A
+// compile-time choice: behind a runtime branch beside an ordinary load of the
+// same address the compiler merges the two and drops the hint.  Measured on
+// MI355X: config 4a 138-139 -> 132-134 us, 5.2 36.6 -> 34.6-34.8 us; with the
+// second operand so loaded too, 4a went back to 138 us; for the broadcast
+// streams (4b, 5.R, first operand laid out as the output) no change.
+template <typename E, int VEC>
+__device__ __forceinline__ void load_stream(const typename E::T* p, float (&v)[VEC]) {
+    if constexpr (VEC == 4 && E::kBytes == 4) {
+        const f32x4 x = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = x[i];
+    } else if constexpr (VEC == 4) {
+        const f16x4 x = __builtin_nontemporal_load(reinterpret_cast<const f16x4*>(p));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = (float)x[i];
+    } else {
+        VecLoad<E, VEC>::load(p, v);
+    }
+}
+
 template <>
 struct VecLoad<F32, 4> {
     __device__ __forceinline__ static void load(const float* p, float (&v)[4]) {
@@ -182,7 +204,9 @@ __global__ __launch_bounds__(kThreads) void product_kernel(ProductArgs p) {
                 aoff = int64_t(vv) * VEC * p.a_inner;
                 boff = int64_t(vv) * VEC * p.b_inner;
             }
-            if constexpr (VEC > 1) {
+            if constexpr (VEC > 1 && !HAS_OUTER) {
+                load_stream<E, VEC>(a + aoff, ra[u]);
+            } else if constexpr (VEC > 1) {
                 VecLoad<E, VEC>::load(a + aoff, ra[u]);
             } else {
                 ra[u][0] = E::to_f32(a[aoff]);
