@@ -92,8 +92,15 @@ __device__ __forceinline__ void put(const RedArgs& a, int64_t o, int64_t c, floa
 }
 
 // Row mode: L consecutive lanes (an aligned segment of the wave) per
-// (output, chunk); lane l of a segment sums groups l, l + L, ...
-template <typename E, int V>
+// (output, chunk); lane l of a segment sums groups l, l + L, ...  Every
+// source element is read once.  NT: non-temporal loads, taken where one load
+// of a segment covers whole 128-byte lines (L x V x element size >= 128);
+// measured on MI355X: [64, 4000000] 177 -> 160 us, [1024, 250000] 177-179 ->
+// 159-160, float16 [1024, 250000] 95-96 -> 85.5-86, [16384, 16000] 181-184
+// -> 162-163, [262144, 1024] 180-181 -> 165-166, [1000000, 256] 169-173 ->
+// 153.5 us; with segments of half a line ([8000000, 32]: 4 lanes x 16
+// bytes) 215 -> 259 us, the line evicted between its two halves' loads.
+template <typename E, int V, bool NT>
 __global__ __launch_bounds__(256) void reduce_row_kernel(RedArgs a) {
     using T = typename E::T;
     const int L = a.L;
@@ -116,7 +123,11 @@ __global__ __launch_bounds__(256) void reduce_row_kernel(RedArgs a) {
     for (; g + (U - 1) * L < g1 && (g + (U - 1) * L + 1) * V <= a.nterm; g += U * L) {
         Vec x[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) x[u] = *reinterpret_cast<const Vec*>(p + (g + u * L) * V);
+        for (int u = 0; u < U; ++u) {
+            const Vec* q = reinterpret_cast<const Vec*>(p + (g + u * L) * V);
+            if constexpr (NT) x[u] = __builtin_nontemporal_load(q);
+            else x[u] = *q;
+        }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             if constexpr (V == 1) {
@@ -129,7 +140,10 @@ __global__ __launch_bounds__(256) void reduce_row_kernel(RedArgs a) {
     }
     // Whole groups one at a time, then the last (partial) group term by term.
     for (; g < g1 && (g + 1) * V <= a.nterm; g += L) {
-        const Vec x = *reinterpret_cast<const Vec*>(p + g * V);
+        const Vec* q = reinterpret_cast<const Vec*>(p + g * V);
+        Vec x;
+        if constexpr (NT) x = __builtin_nontemporal_load(q);
+        else x = *q;
         if constexpr (V == 1) {
             acc = acc + E::to_f32(x);
         } else {
@@ -148,7 +162,10 @@ __global__ __launch_bounds__(256) void reduce_row_kernel(RedArgs a) {
     if (live && lane == 0) put(a, o, c, acc);
 }
 
-// Column mode: one lane per (output, chunk), 64 consecutive outputs per wave.
+// Column mode: one lane per (output, chunk), 64 consecutive outputs per wave;
+// the unrolled loop's loads (a wave reads 64 consecutive elements per term)
+// are non-temporal ([4000000, 64] summed over axis 0: 186-187 -> 167 us on
+// MI355X).
 template <typename E>
 __global__ __launch_bounds__(256) void reduce_col_kernel(RedArgs a, int64_t ngroups) {
     using T = typename E::T;
@@ -169,7 +186,7 @@ __global__ __launch_bounds__(256) void reduce_col_kernel(RedArgs a, int64_t ngro
         for (; t + U <= t1; t += U) {
             T x[U];
 #pragma unroll
-            for (int u = 0; u < U; ++u) x[u] = live ? p[(t + u) * rs] : T(0);
+            for (int u = 0; u < U; ++u) x[u] = live ? __builtin_nontemporal_load(p + (t + u) * rs) : T(0);
 #pragma unroll
             for (int u = 0; u < U; ++u) acc = acc + E::to_f32(x[u]);
         }
@@ -423,12 +440,23 @@ extern "C" int pe_reduce_axes(const pe_reduce_desc* d, const void* src, float* d
         const int64_t blocks = ceil_div(a.nout * a.C * p.L, int64_t(256));
         if (blocks >= (int64_t(1) << 31)) return fail(PE_ERR_UNSUPPORTED, "reduce_axes: too many outputs");
         const dim3 grid{uint32_t(blocks)};
+        const bool nt = int64_t(p.L) * p.V * (f16 ? 2 : 4) >= 128;
         if (f16) {
-            if (p.V == 8) hipLaunchKernelGGL((reduce_row_kernel<F16, 8>), grid, dim3(256), 0, s, a);
-            else hipLaunchKernelGGL((reduce_row_kernel<F16, 1>), grid, dim3(256), 0, s, a);
+            if (p.V == 8) {
+                if (nt) hipLaunchKernelGGL((reduce_row_kernel<F16, 8, true>), grid, dim3(256), 0, s, a);
+                else hipLaunchKernelGGL((reduce_row_kernel<F16, 8, false>), grid, dim3(256), 0, s, a);
+            } else {
+                if (nt) hipLaunchKernelGGL((reduce_row_kernel<F16, 1, true>), grid, dim3(256), 0, s, a);
+                else hipLaunchKernelGGL((reduce_row_kernel<F16, 1, false>), grid, dim3(256), 0, s, a);
+            }
         } else {
-            if (p.V == 4) hipLaunchKernelGGL((reduce_row_kernel<F32, 4>), grid, dim3(256), 0, s, a);
-            else hipLaunchKernelGGL((reduce_row_kernel<F32, 1>), grid, dim3(256), 0, s, a);
+            if (p.V == 4) {
+                if (nt) hipLaunchKernelGGL((reduce_row_kernel<F32, 4, true>), grid, dim3(256), 0, s, a);
+                else hipLaunchKernelGGL((reduce_row_kernel<F32, 4, false>), grid, dim3(256), 0, s, a);
+            } else {
+                if (nt) hipLaunchKernelGGL((reduce_row_kernel<F32, 1, true>), grid, dim3(256), 0, s, a);
+                else hipLaunchKernelGGL((reduce_row_kernel<F32, 1, false>), grid, dim3(256), 0, s, a);
+            }
         }
     } else {
         const int64_t blocks = ceil_div(p.ngroups * a.C, int64_t(4));
