@@ -116,12 +116,13 @@ hipError_t launch_gemm_dl(int dtype, int bm, int bn, int minb, int al, int bl, b
                           hipStream_t s);
 hipError_t launch_gemm_f16(int bm, int bn, int alayout, int blayout, int persist, const GemmArgs& g,
                            hipStream_t s);
-// Short-K kernel (gemm_res_kernel in pe_gemm_dl.h): float16 128x128 tiles,
-// all four 32-k slabs of a K in (96, 128] resident in LDS, one block per tile,
-// operands L_MN or L_K under the gemm_dl_eligible conditions, no split.
+// Short-K kernel (gemm_res_kernel in pe_gemm_dl.h): 128x128 tiles with every
+// k slab resident in LDS (float16: four 32-k slabs, K in (96, 128]; float32:
+// eight 16-k slabs, K in (112, 128]), one block per tile, operands L_MN or
+// L_K under the gemm_dl_eligible conditions, no split.
 // gemm_res_resident: resident blocks per CU (0 when it spilled).
-int gemm_res_resident(int alayout, int blayout);
-hipError_t launch_gemm_res(int alayout, int blayout, const GemmArgs& g, hipStream_t s);
+int gemm_res_resident(int dtype, int alayout, int blayout);
+hipError_t launch_gemm_res(int dtype, int alayout, int blayout, const GemmArgs& g, hipStream_t s);
 // k-split kernel (pe_gemm_ks.h): float32 32x32 or 64x64 tiles, float16 64x64
 // tiles (`tile`), one block per tile and batch, the block's waves splitting
 // K; L_MN or L_K operands under the gemm_dl_eligible conditions, no

@@ -66,12 +66,17 @@
 // 51.6 -> 48.2, 8192 x 16384 x 128 (32) 117.9 -> 92.8; config 3 (128 tiles
 // per CU, its 2.15 GB output the bound) 403-412 -> 439 us, so it keeps the
 // two-stage kernel, whose four blocks per CU keep more stores in flight.
+// The float32 variant (eight 16-k slabs, one block per CU; pe_gemm_desc.tile
+// = 2) is not chosen automatically: on the GDN 16x16 contractions (256 x
+// 128^3, one 128x128 tile per CU) it took 20.8-22.6 us against 18.9-19.6 us
+// for 64x64 tiles of the two-stage kernel at four blocks per CU.
 #ifndef PE_GEMM_RES
 #define PE_GEMM_RES 1
 #endif
 #ifndef PE_GEMM_RES_MAX_TILES_PER_CU
 #define PE_GEMM_RES_MAX_TILES_PER_CU 32
 #endif
+
 
 // float16 GEMMs bound by matrix-core issue take 256x256 tiles (pe_gemm_big.h)
 // when those fill at least one round of CUs.
@@ -488,6 +493,17 @@ GemmChoice choose(const pe_gemm_desc& d, bool dl = false, int al = L_MN, int bl 
     return c;
 }
 
+// Direct-load full slabs address each operand vector by a 32-bit byte offset
+// from the slab's base: (256 rows, 64 bytes of k) of both operands within
+// 2^32 bytes.
+bool dl_off32(const pe_gemm_desc& d) {
+    const int64_t elem = d.dtype == PE_F32 ? 4 : 2;
+    auto span_ok = [&](int64_t rs, int64_t ks) {
+        return rs >= 0 && ks >= 0 && (256 * rs + (64 / elem) * ks + 8) * elem < (int64_t(1) << 32);
+    };
+    return span_ok(d.a_ms, d.a_ks) && span_ok(d.b_ns, d.b_ks);
+}
+
 // Launch of the short-K kernel (gemm_res_kernel) for descriptor d.
 hipError_t launch_res(const pe_gemm_desc& d, const void* a, const void* b, float* c, int64_t nb, int al, int bl,
                       hipStream_t s) {
@@ -504,6 +520,7 @@ hipError_t launch_res(const pe_gemm_desc& d, const void* a, const void* b, float
     g.total_blocks = g.tiles_per_batch * g.nbatch_total;
     g.grid = g.total_blocks;
     g.store_nt = nb * d.M * d.N * 4 >= PE_NT_MIN_BYTES;
+    g.off32 = dl_off32(d);
     g.a_ms = d.a_ms; g.a_ks = d.a_ks; g.b_ks = d.b_ks; g.b_ns = d.b_ns;
     g.c_ms = d.c_ms; g.c_ns = d.c_ns;
     g.nbatch = d.nbatch;
@@ -513,7 +530,7 @@ hipError_t launch_res(const pe_gemm_desc& d, const void* a, const void* b, float
         g.b_bs[i] = d.b_bstride[i];
         g.c_bs[i] = d.c_bstride[i];
     }
-    return launch_gemm_res(al, bl, g, s);
+    return launch_gemm_res(d.dtype, al, bl, g, s);
 }
 
 int classify(int64_t rows, int64_t k, int64_t rs, int64_t ks, const int64_t* bs, int nb,
@@ -537,8 +554,9 @@ int validate_gemm(const pe_gemm_desc& d) {
     if (d.nbatch < 0 || d.nbatch > PE_MAX_DIMS) return fail(PE_ERR_INVALID, "gemm: nbatch out of range");
     if (d.tile != 0 && d.tile != 1 && d.tile != 2 && d.tile != 64 && d.tile != 128 && d.tile != 192 && d.tile != 256)
         return fail(PE_ERR_INVALID, "gemm: tile must be 0, 1, 2, 64, 128, 192 or 256");
-    if (d.tile == 2 && (d.dtype != PE_F16 || d.split_k > 1 || d.K <= 96 || d.K > 128))
-        return fail(PE_ERR_UNSUPPORTED, "gemm: the short-K kernel (tile 2) is float16 only, K in (96, 128], no split");
+    if (d.tile == 2 && (d.split_k > 1 || d.K > 128 || d.K <= (d.dtype == PE_F16 ? 96 : 112)))
+        return fail(PE_ERR_UNSUPPORTED,
+                    "gemm: the short-K kernel (tile 2) takes K in (96, 128] (float16) or (112, 128] (float32), no split");
     if (d.tile == 1 && (d.dtype != PE_F16 || d.split_k > 1))
         return fail(PE_ERR_UNSUPPORTED, "gemm: the 256x256 tile (1) is float16 only, without a K split");
     if (d.tile == 192 && d.dtype != PE_F32)
@@ -658,7 +676,7 @@ extern "C" int pe_gemm(const pe_gemm_desc* d, const void* a, const void* b, floa
         return fail(PE_ERR_UNSUPPORTED,
                     "gemm: the 256x256 tile needs 16-byte vector operands and batch axes that merge into one");
     if (d->tile == 2) {
-        if (!dl || gemm_res_resident(al, bl) < 1)
+        if (!dl || gemm_res_resident(d->dtype, al, bl) < 1)
             return fail(PE_ERR_UNSUPPORTED, "gemm: the short-K kernel (tile 2) needs 16-byte vector operands");
         PE_CHECK_HIP(launch_res(*d, a, b, c, nb, al, bl, s));
         return PE_OK;
@@ -705,10 +723,11 @@ extern "C" int pe_gemm(const pe_gemm_desc* d, const void* a, const void* b, floa
     if (PE_GEMM_RES && dl && d->dtype == PE_F16 && d->split_k == 0 && d->tile == 0 && ch.nsplit == 1 &&
         ch.bm == 128 && ch.bn == 128 && d->K > 96 && d->K <= 128 &&
         nb * ceil_div(d->M, 128) * ceil_div(d->N, 128) <= PE_GEMM_RES_MAX_TILES_PER_CU * cus &&
-        gemm_res_resident(al, bl) >= 1) {
+        gemm_res_resident(d->dtype, al, bl) >= 1) {
         PE_CHECK_HIP(launch_res(*d, a, b, c, nb, al, bl, s));
         return PE_OK;
     }
+
     const int64_t tiles64 = nb * ceil_div(d->M, 64) * ceil_div(d->N, 64);
     const int64_t tiles32 = nb * ceil_div(d->M, 32) * ceil_div(d->N, 32);
     int ks_tile = (4 * tiles64 >= 3 * cus && tiles64 <= PE_GEMM_KS_TILE64_PER_CU * cus) ? 64 : 32;
@@ -770,14 +789,7 @@ extern "C" int pe_gemm(const pe_gemm_desc* d, const void* a, const void* b, floa
         g.b_bs[i] = d->b_bstride[i];
         g.c_bs[i] = d->c_bstride[i];
     }
-    // Direct-load full slabs address each operand vector by a 32-bit byte
-    // offset from the slab's base: (256 rows, BK k) of every operand within
-    // 2^32 bytes.
-    const int64_t elem = d->dtype == PE_F32 ? 4 : 2;
-    auto span_ok = [&](int64_t rs, int64_t ks) {  // a slab is 64 bytes of k
-        return rs >= 0 && ks >= 0 && (256 * rs + (64 / elem) * ks + 8) * elem < (int64_t(1) << 32);
-    };
-    g.off32 = dl && span_ok(d->a_ms, d->a_ks) && span_ok(d->b_ns, d->b_ks);
+    g.off32 = dl && dl_off32(*d);
     hipError_t e = dl                   ? launch_gemm_dl(d->dtype, ch.bm, ch.bn, ch.minb, al, bl, !hbm_bound(*d), g, s)
                    : d->dtype == PE_F32 ? launch_gemm_f32(ch.bm, ch.bn, al, bl, ch.persist, g, s)
                                         : launch_gemm_f16(ch.bm, ch.bn, al, bl, PE_GEMM_F16_PERSIST, g, s);

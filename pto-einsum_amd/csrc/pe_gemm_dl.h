@@ -637,12 +637,24 @@ __global__ __launch_bounds__(kGemmThreads, MINB) void gemm_res_kernel(GemmArgs g
     const int rows_a = g.M - m0, rows_b = g.N - n0;
 
     // Every slab's loads, in slab order (loads complete in issue order, so
-    // vmcnt(n) means all but this wave's last n loads have landed).
+    // vmcnt(n) means all but this wave's last n loads have landed).  Full
+    // slabs load from per-lane 32-bit offsets as in gemm_dl_kernel.
+    const uint32_t lofa = g.off32 ? OA::full_off(g.a_ms, g.a_ks, rows_a, lane, wave) : 0u;
+    const uint32_t lofb = g.off32 ? OB::full_off(g.b_ns, g.b_ks, rows_b, lane, wave) : 0u;
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
         const int kl = g.K - s * BK;
-        OA::load(A + int64_t(s) * BK * g.a_ks, g.a_ms, g.a_ks, rows_a, kl, sa[s], lane, wave);
-        OB::load(B + int64_t(s) * BK * g.b_ks, g.b_ns, g.b_ks, rows_b, kl, sb[s], lane, wave);
+        const T* pa = A + int64_t(s) * BK * g.a_ks;
+        const T* pb = B + int64_t(s) * BK * g.b_ks;
+        const bool full = g.off32 && kl >= BK;
+        if (full && OA::full_ok(rows_a))
+            OA::load_full(pa, OA::chunk_step(g.a_ms, g.a_ks), lofa, lds_addr(sa[s]), wave);
+        else
+            OA::load(pa, g.a_ms, g.a_ks, rows_a, kl, sa[s], lane, wave);
+        if (full && OB::full_ok(rows_b))
+            OB::load_full(pb, OB::chunk_step(g.b_ns, g.b_ks), lofb, lds_addr(sb[s]), wave);
+        else
+            OB::load(pb, g.b_ns, g.b_ks, rows_b, kl, sb[s], lane, wave);
     }
 
     const typename OA::LaneOff loa = OA::lane_off(lane, wm * WM);

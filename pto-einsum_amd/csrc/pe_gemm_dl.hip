@@ -90,21 +90,26 @@ hipError_t launch_gemm_dl(int dtype, int bm, int bn, int minb, int al, int bl, b
     return hipLaunchKernel(dl_kernel(dtype, bm, bn, minb, al, bl), dim3(a.grid), dim3(kGemmThreads), args, 0, s);
 }
 
-// Short-K all-resident kernel (gemm_res_kernel): float16 128x128 tiles with
-// four resident 32-k slabs (K in (96, 128]), two blocks per CU.
-static const void* res_kernel(int al, int bl) {
+// Short-K all-resident kernel (gemm_res_kernel): 128x128 tiles with every k
+// slab of K resident in LDS.  float16: four 32-k slabs (K in (96, 128]), two
+// blocks per CU; float32: eight 16-k slabs (K in (112, 128]), one block per CU.
+template <typename E, int NS, int MINB>
+static const void* res_kernel_t(int al, int bl) {
     if (al == L_MN)
-        return bl == L_MN ? reinterpret_cast<const void*>(&gemm_res_kernel<F16, 128, 128, L_MN, L_MN, 4, 2>)
-                          : reinterpret_cast<const void*>(&gemm_res_kernel<F16, 128, 128, L_MN, L_K, 4, 2>);
-    return bl == L_MN ? reinterpret_cast<const void*>(&gemm_res_kernel<F16, 128, 128, L_K, L_MN, 4, 2>)
-                      : reinterpret_cast<const void*>(&gemm_res_kernel<F16, 128, 128, L_K, L_K, 4, 2>);
+        return bl == L_MN ? reinterpret_cast<const void*>(&gemm_res_kernel<E, 128, 128, L_MN, L_MN, NS, MINB>)
+                          : reinterpret_cast<const void*>(&gemm_res_kernel<E, 128, 128, L_MN, L_K, NS, MINB>);
+    return bl == L_MN ? reinterpret_cast<const void*>(&gemm_res_kernel<E, 128, 128, L_K, L_MN, NS, MINB>)
+                      : reinterpret_cast<const void*>(&gemm_res_kernel<E, 128, 128, L_K, L_K, NS, MINB>);
+}
+static const void* res_kernel(int dtype, int al, int bl) {
+    return dtype == PE_F32 ? res_kernel_t<F32, 8, 1>(al, bl) : res_kernel_t<F16, 4, 2>(al, bl);
 }
 
-int gemm_res_resident(int al, int bl) {
-    static int cache[4] = {-1, -1, -1, -1};
-    int& c = cache[(al == L_K) * 2 + (bl == L_K)];
+int gemm_res_resident(int dtype, int al, int bl) {
+    static int cache[2][4] = {{-1, -1, -1, -1}, {-1, -1, -1, -1}};
+    int& c = cache[dtype == PE_F32][(al == L_K) * 2 + (bl == L_K)];
     if (c < 0) {
-        const void* k = res_kernel(al, bl);
+        const void* k = res_kernel(dtype, al, bl);
         hipFuncAttributes at{};
         int n = 0;
         if (hipFuncGetAttributes(&at, k) != hipSuccess || at.localSizeBytes > PE_GEMM_DL_MAX_SPILL ||
@@ -115,11 +120,11 @@ int gemm_res_resident(int al, int bl) {
     return c;
 }
 
-hipError_t launch_gemm_res(int al, int bl, const GemmArgs& g, hipStream_t s) {
-    if (gemm_res_resident(al, bl) < 1) return hipErrorInvalidConfiguration;
+hipError_t launch_gemm_res(int dtype, int al, int bl, const GemmArgs& g, hipStream_t s) {
+    if (gemm_res_resident(dtype, al, bl) < 1) return hipErrorInvalidConfiguration;
     GemmArgs a = g;
     void* args[] = {&a};
-    return hipLaunchKernel(res_kernel(al, bl), dim3(a.total_blocks), dim3(kGemmThreads), args, 0, s);
+    return hipLaunchKernel(res_kernel(dtype, al, bl), dim3(a.total_blocks), dim3(kGemmThreads), args, 0, s);
 }
 
 }  // namespace pe

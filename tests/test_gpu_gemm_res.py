@@ -1,11 +1,11 @@
-"""The short-K GEMM kernel (float16, K in (96, 128]: every k slab of a 128x128
-tile resident in LDS, all loads issued up front; forced with
-pe_gemm_desc.tile = 2 at sizes the automatic choice sends elsewhere): every
-operand layout pairing, K tails inside the last slab, partial tiles in M and
-N and batches, against a float64 reference, with run-to-run equality (the
-reference checks its batched matmul the same way, test_einsum.py:244-364);
-and config 5.1 and config-3-shaped products through the public einsum, which
-choose it."""
+"""The short-K GEMM kernel (every k slab of a 128x128 tile resident in LDS,
+all loads issued up front: float16 with K in (96, 128], float32 with K in
+(112, 128]; forced with pe_gemm_desc.tile = 2 at sizes the automatic choice
+sends elsewhere): every operand layout pairing, K tails inside the last slab,
+partial tiles in M and N and batches, against a float64 reference, with
+run-to-run equality (the reference checks its batched matmul the same way,
+test_einsum.py:244-364); and config 5.1 and a config-3-shaped product
+through the public einsum, which choose the float16 variant."""
 import ctypes
 
 import pytest
@@ -32,20 +32,27 @@ def test_refused_outside_its_range():
                         M=128, N=128, K=64, a_ms=64, a_ks=1, b_ks=128, b_ns=1, c_ms=128, c_ns=1,
                         a_numel=128 * 64, b_numel=64 * 128, c_numel=128 * 128, tile=2)
     assert lib.pe_gemm(ctypes.byref(abi.gemm_desc(d)), None, None, None, None, 0, None) == -3
-    d.dtype, d.K = launch.DT_F32, 128
+    d.dtype, d.K = launch.DT_F32, 112
+    assert lib.pe_gemm(ctypes.byref(abi.gemm_desc(d)), None, None, None, None, 0, None) == -3
+    d.K = 160
     assert lib.pe_gemm(ctypes.byref(abi.gemm_desc(d)), None, None, None, None, 0, None) == -3
 
 
 @pytest.mark.parametrize("al,bl", [("mn", "mn"), ("mn", "k"), ("k", "mn"), ("k", "k")])
-@pytest.mark.parametrize("nb,M,N,K", [(3, 128, 128, 128), (2, 200, 136, 120), (5, 136, 264, 104),
-                                      (1, 1000, 384, 128), (4, 136, 72, 112)])
-def test_short_k_kernel_against_float64(al, bl, nb, M, N, K):
+@pytest.mark.parametrize("dt,nb,M,N,K", [("f16", 3, 128, 128, 128), ("f16", 2, 200, 136, 120),
+                                         ("f16", 5, 136, 264, 104), ("f16", 1, 1000, 384, 128),
+                                         ("f16", 4, 136, 72, 112), ("f32", 3, 128, 128, 128),
+                                         ("f32", 2, 200, 136, 124), ("f32", 5, 136, 264, 116),
+                                         ("f32", 1, 1000, 384, 128), ("f32", 4, 132, 68, 120)])
+def test_short_k_kernel_against_float64(al, bl, dt, nb, M, N, K):
     g = torch.Generator().manual_seed(nb * 1000 + M + N + K)
-    A = (torch.randn(nb, M, K, generator=g) / 8).half()
-    B = (torch.randn(nb, K, N, generator=g) / 8).half()
+    tdt = torch.float16 if dt == "f16" else torch.float32
+    A = (torch.randn(nb, M, K, generator=g) / 8).to(tdt)
+    B = (torch.randn(nb, K, N, generator=g) / 8).to(tdt)
     a_buf, a_ms, a_ks = (A.transpose(1, 2).contiguous(), 1, M) if al == "mn" else (A.contiguous(), K, 1)
     b_buf, b_ks, b_ns = (B.contiguous(), N, 1) if bl == "mn" else (B.transpose(1, 2).contiguous(), 1, K)
-    d = launch.GemmDesc(dtype=launch.DT_F16, batch_shape=[nb], a_bstride=[M * K], b_bstride=[K * N],
+    d = launch.GemmDesc(dtype=launch.DT_F16 if dt == "f16" else launch.DT_F32, batch_shape=[nb],
+                        a_bstride=[M * K], b_bstride=[K * N],
                         c_bstride=[M * N], M=M, N=N, K=K, a_ms=a_ms, a_ks=a_ks, b_ks=b_ks, b_ns=b_ns,
                         c_ms=N, c_ns=1, a_numel=nb * M * K, b_numel=nb * K * N, c_numel=nb * M * N, tile=2)
     lib = abi.bind()
@@ -64,14 +71,15 @@ def test_short_k_kernel_against_float64(al, bl, nb, M, N, K):
     assert all(torch.equal(outs[0], o) for o in outs[1:])
 
 
-@pytest.mark.parametrize("eq,s0,s1", [("tn,sn->ts", (4096, 128), (4096, 128)),
-                                      ("bshd,bthd->bsht", (2, 512, 8, 128), (2, 384, 8, 128))])
-def test_public_einsum_shapes_that_take_it(eq, s0, s1):
+@pytest.mark.parametrize("eq,s0,s1,dt", [("tn,sn->ts", (4096, 128), (4096, 128), "f16"),
+                                         ("bshd,bthd->bsht", (2, 512, 8, 128), (2, 384, 8, 128), "f16")])
+def test_public_einsum_shapes_that_take_it(eq, s0, s1, dt):
     """Config 5.1 itself and a config-3-shaped product (two batch axes, the
     fused permuted store) through einsum(), against a float64 reference."""
     g = torch.Generator().manual_seed(51)
-    x = (torch.randn(s0, generator=g) / 8).half()
-    y = (torch.randn(s1, generator=g) / 8).half()
+    tdt = torch.float16 if dt == "f16" else torch.float32
+    x = (torch.randn(s0, generator=g) / 8).to(tdt)
+    y = (torch.randn(s1, generator=g) / 8).to(tdt)
     got = einsum(eq, x.cuda(), y.cuda()).cpu().double()
     want = torch.einsum(eq, x.double(), y.double())
     bound = torch.einsum(eq, x.double().abs(), y.double().abs())
