@@ -234,9 +234,13 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_big_kernel(GemmArgs g) {
     constexpr uint32_t STAGE = OA::STAGE_BYTES + OB::STAGE_BYTES;   // one slab of A and B: 32 KB
     constexpr uint32_t RING = kBigStages * STAGE;                   // 128 KB
     static_assert((RING & (RING - 1)) == 0, "stage offsets wrap with a mask");
-    static_assert(RING <= 160 * 1024, "LDS budget");
+    // Past the ring: one 1 KB chunk per wave that the streamed loads of a
+    // slab with nothing to stream write into (never read), so those loads
+    // need no branch.
+    constexpr uint32_t SPARE = 4 * 1024;
+    static_assert(RING + SPARE <= 160 * 1024, "LDS budget");
     static_assert(OA::NI == 4 && OB::NI == 4, "the schedule places four loads per operand per slab");
-    __shared__ __attribute__((aligned(1024))) _Float16 lds[RING / 2];
+    __shared__ __attribute__((aligned(1024))) _Float16 lds[(RING + SPARE) / 2];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -399,10 +403,19 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_big_kernel(GemmArgs g) {
             // unless it has a K tail (then issued whole, here).
             const bool fast = lvalid && ls != tail_slab;
             if (!fast) issue_whole();
-            const _Float16* sa = pa;
-            const _Float16* sb = pb;
+            // A slab with nothing to stream (the block's last slabs, or the
+            // load slab has a K tail and went whole above) still issues its
+            // eight streamed loads, from the operands' own bases (the tile's
+            // full-slab offsets stay inside the operand from there: the
+            // tile's base is at or above it) into the spare chunk: a branch
+            // around each load made the wave refetch instructions between
+            // MFMAs, with one wave per SIMD leaving the matrix core idle.
+            const _Float16* sa = fast ? pa : static_cast<const _Float16*>(g.a);
+            const _Float16* sb = fast ? pb : static_cast<const _Float16*>(g.b);
+            const uint32_t spare = lds0 + RING + uint32_t(wave) * 1024u;
             const uint32_t la = lds0 + lstage + uint32_t(wave) * 1024u;
             const uint32_t lb = la + OA::STAGE_BYTES;
+            const uint32_t lda = fast ? 4096u : 0u;  // LDS step between a wave's loads of a slab
             const uint32_t ba = lds0 + cstage + wa_off, bb = lds0 + cstage + OA::STAGE_BYTES + wb_off;
             const uint32_t na = lds0 + nstage + wa_off, nb = lds0 + nstage + OA::STAGE_BYTES + wb_off;
             __builtin_amdgcn_s_setprio(1);
@@ -422,7 +435,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_big_kernel(GemmArgs g) {
                 acc[t / 4][t % 4] =
                     __builtin_amdgcn_mfma_f32_32x32x16_f16(f0a[t / 4], f0b[t % 4], acc[t / 4][t % 4], 0, 0, 0);
                 if (t % 2 == 1) read_unit(f1a, f1b, ba, bb, t / 2, 1);
-                else if (t % 4 == 0 && fast) OA::load1(sa, offa[t / 4], la + uint32_t(t / 4) * 4096u);
+                else if (t % 4 == 0) OA::load1(sa, offa[t / 4], (fast ? la : spare) + uint32_t(t / 4) * lda);
                 __builtin_amdgcn_sched_barrier(0);
             }
 #pragma unroll
@@ -435,7 +448,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_big_kernel(GemmArgs g) {
                 // leave the compiler unsure how many LDS reads are in flight,
                 // so it would wait for all of them before the MFMAs below.)
                 if (t % 2 == 1) read_unit(f0a, f0b, na, nb, t / 2, 0);
-                else if (t % 4 == 2 && fast) OB::load1(sb, offb[t / 4], lb + uint32_t(t / 4) * 4096u);
+                else if (t % 4 == 2) OB::load1(sb, offb[t / 4], (fast ? lb : spare) + uint32_t(t / 4) * lda);
                 // (After the slab's last load: a move to the next tile
                 // recomputes the load offsets.)
                 if (t == 15 && fast) advance_load();
