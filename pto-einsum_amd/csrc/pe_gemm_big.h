@@ -224,7 +224,9 @@ __device__ __forceinline__ const _Float16* big_uniform(const _Float16* p) {
     return reinterpret_cast<const _Float16*>((uint64_t(hi) << 32) | uint64_t(lo));
 }
 
-template <int AL, int BL>
+// TAIL: K is not a whole number of 32-k slabs (the last slab of each tile
+// has a K tail); without one, the per-slab tail checks are compiled out.
+template <int AL, int BL, bool TAIL>
 __global__ __launch_bounds__(kGemmThreads, 1) void gemm_big_kernel(GemmArgs g) {
     using OA = BigOperand<AL>;
     using OB = BigOperand<BL>;
@@ -250,7 +252,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_big_kernel(GemmArgs g) {
     const uint32_t lds0 = uint32_t(reinterpret_cast<uintptr_t>(
         (const __attribute__((address_space(3))) _Float16*)(lds)));
     const int nslabs = (g.K + BK - 1) / BK;                  // slabs per tile (every tile has all of K)
-    const int tail_slab = g.K % BK ? nslabs - 1 : nslabs;    // the slab with a K tail, if any
+    const int tail_slab = TAIL ? nslabs - 1 : nslabs;        // the slab with a K tail, if any
     // Byte steps of the load pointers per slab.
     const int64_t step_a = int64_t(BK) * g.a_ks, step_b = int64_t(BK) * g.b_ks;
 
@@ -317,7 +319,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_big_kernel(GemmArgs g) {
         lstage = (lstage + STAGE) & (RING - 1);
         pa += step_a;
         pb += step_b;
-        if (++ls == nslabs) {
+        if (__builtin_expect(++ls == nslabs, 0)) {
             lbid += walk.step;
             lvalid = lbid < walk.end;
             if (lvalid) {
@@ -334,7 +336,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_big_kernel(GemmArgs g) {
     // tail (every address clamped).
     auto issue_whole = [&]() {
         if (!lvalid) return;
-        if (ls == tail_slab) {
+        if (TAIL && ls == tail_slab) {
             const int kl = g.K - ls * BK;
             OA::load(pa, g.a_ms, g.a_ks, lt.rows_a, kl, lds0 + lstage, lane, wave);
             OB::load(pb, g.b_ns, g.b_ks, lt.rows_b, kl, lds0 + lstage + OA::STAGE_BYTES, lane, wave);
@@ -350,7 +352,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_big_kernel(GemmArgs g) {
     // Zeroes the K tail of the stage at byte offset `stage` (the slab with
     // index `slab` in its tile) when it has one.
     auto tail_fix = [&](int slab, uint32_t stage) {
-        if (slab == tail_slab) {
+        if (TAIL && slab == tail_slab) {
             const int k_left = g.K - slab * BK;
             OA::zero_tail(reinterpret_cast<_Float16*>(lds) + stage / 2, k_left, tid);
             OB::zero_tail(reinterpret_cast<_Float16*>(lds) + (stage + OA::STAGE_BYTES) / 2, k_left, tid);
@@ -393,16 +395,16 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_big_kernel(GemmArgs g) {
             // then makes every wave's visible and frees the stage read two
             // slabs ago, which this iteration refills.  (Loads complete in
             // issue order; at most the slab after next is in flight.)
-            if (gi - gs > 2) asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
+            if (__builtin_expect(gi - gs > 2, 1)) asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
             else asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
             const bool last = cs + 1 == nslabs;
             const bool more = !last || cbid + walk.step < walk.end;
             const uint32_t nstage = (cstage + STAGE) & (RING - 1);
-            if (more) tail_fix(last ? 0 : cs + 1, nstage);
+            if (TAIL && more) tail_fix(last ? 0 : cs + 1, nstage);
             // The load slab of this iteration: streamed between the MFMAs
             // unless it has a K tail (then issued whole, here).
-            const bool fast = lvalid && ls != tail_slab;
-            if (!fast) issue_whole();
+            const bool fast = lvalid && (!TAIL || ls != tail_slab);
+            if (TAIL && !fast) issue_whole();
             // A slab with nothing to stream (the block's last slabs, or the
             // load slab has a K tail and went whole above) still issues its
             // eight streamed loads, from the operands' own bases (the tile's
@@ -457,7 +459,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_big_kernel(GemmArgs g) {
             __builtin_amdgcn_s_setprio(0);
             cstage = nstage;
             ++gs;
-            if (last) break;
+            if (__builtin_expect(last, 0)) break;
         }
 
         // Epilogue: the accumulators straight to the output.

@@ -3,27 +3,37 @@
 // and the persistent launch, one block per CU.
 #include "pe_gemm_big.h"
 
+#include <algorithm>
+
 namespace pe {
 
-static const void* big_kernel(int al, int bl) {
+template <bool TAIL>
+static const void* big_kernel_t(int al, int bl) {
     if (al == L_K)
-        return bl == L_K ? reinterpret_cast<const void*>(&gemm_big_kernel<L_K, L_K>)
-                         : reinterpret_cast<const void*>(&gemm_big_kernel<L_K, L_MN>);
-    return bl == L_K ? reinterpret_cast<const void*>(&gemm_big_kernel<L_MN, L_K>)
-                     : reinterpret_cast<const void*>(&gemm_big_kernel<L_MN, L_MN>);
+        return bl == L_K ? reinterpret_cast<const void*>(&gemm_big_kernel<L_K, L_K, TAIL>)
+                         : reinterpret_cast<const void*>(&gemm_big_kernel<L_K, L_MN, TAIL>);
+    return bl == L_K ? reinterpret_cast<const void*>(&gemm_big_kernel<L_MN, L_K, TAIL>)
+                     : reinterpret_cast<const void*>(&gemm_big_kernel<L_MN, L_MN, TAIL>);
+}
+static const void* big_kernel(int al, int bl, bool tail) {
+    return tail ? big_kernel_t<true>(al, bl) : big_kernel_t<false>(al, bl);
 }
 
+// Resident blocks per CU of both variants (0 when either spilled).
 int gemm_big_resident(int al, int bl) {
     static int cache[4] = {-1, -1, -1, -1};
     int& c = cache[(al == L_K) * 2 + (bl == L_K)];
     if (c < 0) {
+        c = 1 << 30;
+        for (bool tail : {false, true}) {
         hipFuncAttributes at{};
         int n = 0;
-        const void* k = big_kernel(al, bl);
+        const void* k = big_kernel(al, bl, tail);
         if (hipFuncGetAttributes(&at, k) != hipSuccess || at.localSizeBytes > 16 ||
             hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k, kGemmThreads, 0) != hipSuccess || n < 1)
             n = 0;
-        c = n;
+        c = std::min(c, n);
+        }
     }
     return c;
 }
@@ -35,7 +45,7 @@ hipError_t launch_gemm_big(int al, int bl, const GemmArgs& g, hipStream_t s) {
     const uint32_t cap = uint32_t(cu_count()) * uint32_t(resident);
     if (a.grid > cap) a.grid = cap;
     void* args[] = {&a};
-    return hipLaunchKernel(big_kernel(al, bl), dim3(a.grid), dim3(kGemmThreads), args, 0, s);
+    return hipLaunchKernel(big_kernel(al, bl, a.K % 32 != 0), dim3(a.grid), dim3(kGemmThreads), args, 0, s);
 }
 
 }  // namespace pe
