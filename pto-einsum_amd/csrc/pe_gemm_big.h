@@ -407,11 +407,11 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_big_kernel(GemmArgs g) {
             if (TAIL && !fast) issue_whole();
             // A slab with nothing to stream (the block's last slabs, or the
             // load slab has a K tail and went whole above) still issues its
-            // eight streamed loads, from the operands' own bases (the tile's
-            // full-slab offsets stay inside the operand from there: the
-            // tile's base is at or above it) into the spare chunk: a branch
-            // around each load made the wave refetch instructions between
-            // MFMAs, with one wave per SIMD leaving the matrix core idle.
+            // eight streamed loads, each lane reading the operand's first 16
+            // bytes (in bounds for any shape), into the spare chunk: a
+            // branch around each load made the wave refetch instructions
+            // between MFMAs, with one wave per SIMD leaving the matrix core
+            // idle.
             const _Float16* sa = fast ? pa : static_cast<const _Float16*>(g.a);
             const _Float16* sb = fast ? pb : static_cast<const _Float16*>(g.b);
             const uint32_t spare = lds0 + RING + uint32_t(wave) * 1024u;
@@ -437,7 +437,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_big_kernel(GemmArgs g) {
                 acc[t / 4][t % 4] =
                     __builtin_amdgcn_mfma_f32_32x32x16_f16(f0a[t / 4], f0b[t % 4], acc[t / 4][t % 4], 0, 0, 0);
                 if (t % 2 == 1) read_unit(f1a, f1b, ba, bb, t / 2, 1);
-                else if (t % 4 == 0) OA::load1(sa, offa[t / 4], (fast ? la : spare) + uint32_t(t / 4) * lda);
+                else if (t % 4 == 0) OA::load1(sa, fast ? offa[t / 4] : 0u, (fast ? la : spare) + uint32_t(t / 4) * lda);
                 __builtin_amdgcn_sched_barrier(0);
             }
 #pragma unroll
@@ -450,7 +450,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_big_kernel(GemmArgs g) {
                 // leave the compiler unsure how many LDS reads are in flight,
                 // so it would wait for all of them before the MFMAs below.)
                 if (t % 2 == 1) read_unit(f0a, f0b, na, nb, t / 2, 0);
-                else if (t % 4 == 2) OB::load1(sb, offb[t / 4], (fast ? lb : spare) + uint32_t(t / 4) * lda);
+                else if (t % 4 == 2) OB::load1(sb, fast ? offb[t / 4] : 0u, (fast ? lb : spare) + uint32_t(t / 4) * lda);
                 // (After the slab's last load: a move to the next tile
                 // recomputes the load offsets.)
                 if (t == 15 && fast) advance_load();
