@@ -7,16 +7,19 @@
 
 namespace pe {
 
+// M16: the 16x16x32 schedule, for k-contiguous A and B with an even number
+// of 32-k slabs per tile.
 template <bool TAIL>
-static const void* big_kernel_t(int al, int bl) {
+static const void* big_kernel_t(int al, int bl, bool m16) {
     if (al == L_K)
-        return bl == L_K ? reinterpret_cast<const void*>(&gemm_big_kernel<L_K, L_K, TAIL>)
-                         : reinterpret_cast<const void*>(&gemm_big_kernel<L_K, L_MN, TAIL>);
-    return bl == L_K ? reinterpret_cast<const void*>(&gemm_big_kernel<L_MN, L_K, TAIL>)
-                     : reinterpret_cast<const void*>(&gemm_big_kernel<L_MN, L_MN, TAIL>);
+        return bl == L_K ? (m16 ? reinterpret_cast<const void*>(&gemm_big_kernel<L_K, L_K, TAIL, true>)
+                                : reinterpret_cast<const void*>(&gemm_big_kernel<L_K, L_K, TAIL, false>))
+                         : reinterpret_cast<const void*>(&gemm_big_kernel<L_K, L_MN, TAIL, false>);
+    return bl == L_K ? reinterpret_cast<const void*>(&gemm_big_kernel<L_MN, L_K, TAIL, false>)
+                     : reinterpret_cast<const void*>(&gemm_big_kernel<L_MN, L_MN, TAIL, false>);
 }
-static const void* big_kernel(int al, int bl, bool tail) {
-    return tail ? big_kernel_t<true>(al, bl) : big_kernel_t<false>(al, bl);
+static const void* big_kernel(int al, int bl, bool tail, bool m16) {
+    return tail ? big_kernel_t<true>(al, bl, m16) : big_kernel_t<false>(al, bl, m16);
 }
 
 // Resident blocks per CU of both variants (0 when either spilled).
@@ -25,15 +28,16 @@ int gemm_big_resident(int al, int bl) {
     int& c = cache[(al == L_K) * 2 + (bl == L_K)];
     if (c < 0) {
         c = 1 << 30;
-        for (bool tail : {false, true}) {
-        hipFuncAttributes at{};
-        int n = 0;
-        const void* k = big_kernel(al, bl, tail);
-        if (hipFuncGetAttributes(&at, k) != hipSuccess || at.localSizeBytes > 16 ||
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k, kGemmThreads, 0) != hipSuccess || n < 1)
-            n = 0;
-        c = std::min(c, n);
-        }
+        for (bool tail : {false, true})
+            for (bool m16 : {false, true}) {
+                hipFuncAttributes at{};
+                int n = 0;
+                const void* k = big_kernel(al, bl, tail, m16);
+                if (hipFuncGetAttributes(&at, k) != hipSuccess || at.localSizeBytes > 16 ||
+                    hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k, kGemmThreads, 0) != hipSuccess || n < 1)
+                    n = 0;
+                c = std::min(c, n);
+            }
     }
     return c;
 }
@@ -45,7 +49,8 @@ hipError_t launch_gemm_big(int al, int bl, const GemmArgs& g, hipStream_t s) {
     const uint32_t cap = uint32_t(cu_count()) * uint32_t(resident);
     if (a.grid > cap) a.grid = cap;
     void* args[] = {&a};
-    return hipLaunchKernel(big_kernel(al, bl, a.K % 32 != 0), dim3(a.grid), dim3(kGemmThreads), args, 0, s);
+    const bool m16 = al == L_K && bl == L_K && ((a.K + 31) / 32) % 2 == 0;
+    return hipLaunchKernel(big_kernel(al, bl, a.K % 32 != 0, m16), dim3(a.grid), dim3(kGemmThreads), args, 0, s);
 }
 
 }  // namespace pe

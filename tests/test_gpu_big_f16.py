@@ -31,7 +31,7 @@ def _operands(nbatch, M, N, K, layout_a, layout_b, seed):
 
 LAYOUTS = [("k", "mn"), ("k", "k"), ("mn", "mn"), ("mn", "k")]
 SHAPES = [(1, 512, 512, 64), (2, 520, 264, 104), (3, 256, 768, 1000), (1, 2048, 2048, 96),
-          (9, 1280, 2048, 40), (1, 264, 256, 24)]
+          (9, 1280, 2048, 40), (1, 264, 256, 24), (9, 1280, 2048, 64), (4, 2560, 2048, 256)]
 
 
 @pytest.mark.parametrize("layout_a,layout_b", LAYOUTS, ids=lambda v: v)
