@@ -20,6 +20,15 @@ are HBM figures, not cache figures.  Einsum cases call the per-shape
 library's run_einsum_exec with an explicit output per operand set; the
 headline steps rotate the same way.
 
+Clocks: after an idle gap (host-side setup between cases) the GPU's clock
+ramps back up over about 25 ms of sustained work: config 2's launches take
+346 us right after a 1 s pause and settle at 292 us (128x256 tiles) or 278 us
+(128x128) after about 80 launches.  Every figure here is taken at the
+settled clock: the headline does ``--warmup`` untimed steps first (default
+200, about 60 ms), and each graph-replayed case replays its graph back to
+back for at least 50 ms before the timed replays, which also run back to
+back (one event pair per replay, one synchronisation after the last).
+
 ``per_config`` adds every other benchmark equation at full size with its own
 binding roof (HBM bytes or MFMA flops).  Those kernels run for tens of
 microseconds, less than one Python-level call costs, so the rotation's calls
@@ -50,7 +59,7 @@ counters on ``--copy-probe`` (a plain copy of known size); the file names
 the kernel it was measured on, and the line carries that name beside it.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-configs]
-       python bench.py --profile CASE   # one case, eager calls, for rocprofv3
+       python bench.py --profile CASE   # one case, eager calls (after ~50 ms of warm-up calls), for rocprofv3
        python bench.py --list-cases
        python bench.py --copy-probe     # counter calibration: one 1 GiB copy
 """
@@ -80,7 +89,7 @@ def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
     ap.add_argument("--steps", type=int, default=30)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-configs", action="store_true", help="headline workload only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
@@ -134,10 +143,12 @@ def time_runner(run, sets, steps, warmup):
     return per, t0.elapsed_time(t1)
 
 
-def time_graph(call, sets, reps=5):
+def time_graph(call, sets, reps=5, warm_ms=50.0):
     """GPU time (ms) per call: one call per operand set captured in one HIP
-    graph, the graph replayed between two events `reps` times; the median
-    replay time divided by the number of calls."""
+    graph; the graph is replayed back to back for at least `warm_ms` (the
+    clock's ramp after an idle gap), then `reps` more times back to back,
+    each between its own pair of events; the median replay time divided by
+    the number of calls."""
     import torch
 
     for s in sets[:2]:
@@ -147,28 +158,45 @@ def time_graph(call, sets, reps=5):
     with torch.cuda.graph(g):
         for s in sets:
             call(*s)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
     g.replay()
+    e1.record()
     torch.cuda.synchronize()
-    per = []
-    for _ in range(reps):
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record()
+    once = max(e0.elapsed_time(e1), 1e-3)
+    for _ in range(min(100000, int(math.ceil(warm_ms / once)))):
         g.replay()
-        e1.record()
-        torch.cuda.synchronize()
-        per.append(e0.elapsed_time(e1) / len(sets))
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for a, b in ev:
+        a.record()
+        g.replay()
+        b.record()
+    torch.cuda.synchronize()
+    per = [a.elapsed_time(b) / len(sets) for a, b in ev]
     del g
     return statistics.median(per)
 
 
-def run_eager(call, sets, calls):
-    """Profiling mode: `calls` eager calls rotating over the sets."""
+def run_eager(call, sets, calls, warm_ms=50.0):
+    """Profiling mode: eager calls rotating over the sets, first for at least
+    `warm_ms` of GPU time (the clock's ramp), then `calls` more (the ones a
+    profile summary averages); returns the number of warm-up calls."""
     import torch
 
-    for i in range(calls):
+    call(*sets[0])
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    call(*sets[1 % len(sets)])
+    e1.record()
+    torch.cuda.synchronize()
+    warm = min(5000, int(math.ceil(warm_ms / max(e0.elapsed_time(e1), 1e-3))))
+    for i in range(warm + calls):
         call(*sets[i % len(sets)])
     torch.cuda.synchronize()
+    return warm + 2
 
 
 def copy_probe():
@@ -631,9 +659,10 @@ def measure(case, dev, steps, warmup, profile_calls=0):
     nsets = n_sets(set_bytes)
     sets = replicate(operands, nsets)
     if profile_calls:
-        log(f"bench: profiling {case.name}: {profile_calls} eager calls over {nsets} rotated sets")
-        run_eager(call, sets, profile_calls)
-        return None
+        warm = run_eager(call, sets, profile_calls)
+        log(f"bench: profiling {case.name}: {warm} warm-up and {profile_calls} counted eager calls over {nsets} "
+            f"rotated sets")
+        return warm
     ms = time_graph(call, sets, reps=max(3, steps // 6))
     row = case.finish(ms, operands, nsets)
     del sets, operands, call
@@ -1036,8 +1065,8 @@ def main():
         found = [c for cs in groups.values() for c in cs if c.name == args.profile]
         if not found:
             sys.exit(f"bench.py: no case {args.profile!r} (see --list-cases)")
-        measure(found[0], dev, args.steps, args.warmup, profile_calls=max(1, args.steps))
-        print(json.dumps({"profiled": args.profile, "calls": max(1, args.steps)}))
+        warm = measure(found[0], dev, args.steps, args.warmup, profile_calls=max(1, args.steps))
+        print(json.dumps({"profiled": args.profile, "calls": max(1, args.steps), "warm_calls": warm}))
         return
 
     # ---- headline: config 2, rotated operand sets ----

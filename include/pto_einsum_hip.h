@@ -128,10 +128,11 @@ int pe_permute(const pe_permute_desc* d, const void* src, void* dst, void* strea
 int64_t pe_gemm_workspace_bytes(const pe_gemm_desc* d);
 int pe_gemm(const pe_gemm_desc* d, const void* a, const void* b, float* c, void* ws,
             int64_t ws_bytes, void* stream);
-/* The tile and K split the workspace query sizes for (no counterpart in the
- * reference; for tests and tuning): info[0..3] = tile rows, tile columns,
- * K splits, k per split.  Operand layouts can change the kernel but not the
- * split. */
+/* The tile and K split pe_gemm takes for these extents and strides, operand
+ * pointers taken as 16-byte aligned (no counterpart in the reference; for
+ * tests and tuning): info[0..3] = tile rows, tile columns, K splits, k per
+ * split (256 x 256 for the large float16 kernel).  The split, and so the
+ * workspace size, is the same for every operand layout. */
 int pe_gemm_choice(const pe_gemm_desc* d, int64_t* info);
 
 /* Fused linear-attention chain.  No single entry point of the reference

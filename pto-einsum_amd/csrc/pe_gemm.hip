@@ -329,15 +329,18 @@ GemmChoice choose(const pe_gemm_desc& d, bool dl = false, int al = L_MN, int bl 
             }
         }
         c.bn = c.bm;
-        if (PE_GEMM_BIG && dl && c.bm == 128 && !hbm_bound(d)) {
-            // Direct-load 256x128 / 128x256 tiles come in two register
-            // budgets, three or two resident blocks per CU.  Like the tiles
-            // below they only pay off in whole rounds: config 2 (768 tiles)
-            // fills one round at three per CU, 4096^2 (512 tiles) one round
-            // at two per CU, where 512 blocks with three slots per CU left
-            // CUs with one block next to CUs with three (-18 %).  Measured
-            // on one MI355X for config 2: 346-354 us for the four 256-wide
-            // variants, 369 us for the staged kernel's 128x128 tiles.  Both
+        if (PE_GEMM_BIG && dl && c.bm == 128 && !hbm_bound(d) && d.dtype == PE_F16) {
+            // Direct-load float16 256x128 / 128x256 tiles come in two
+            // register budgets, three or two resident blocks per CU, and
+            // pay off in whole rounds (4096^2 x 1024: 512 tiles, one round
+            // at two per CU, 43.5 us against 47.5 for 128x128; 4 x 2048^2 x
+            // 2048 84 against 97; 3072^2 x 2048 51.7 against 54.6, steady
+            // clocks).  Float32 keeps the direct-load 128x128 tiles (four
+            // blocks per CU): at steady clocks they beat the 256-wide ones
+            // on every MFMA-bound shape measured (config 2 278 against 292
+            // us, 8 x 2048^2 x 512 245 against 262, 4096^3 919 against 928,
+            // 4096 x 6144 x 1024 356 against 362; 4 x 2048^2 x 2048 with
+            // both operands k-contiguous 483 against 480).  Both
             // orientations are candidates, the one along the longer output
             // axis first (their register allocations differ; an
             // instantiation that spills reports no residency).
@@ -599,7 +602,19 @@ extern "C" int pe_gemm_choice(const pe_gemm_desc* d, int64_t* info) {
     if (!d || !info) return pe::fail(PE_ERR_INVALID, "gemm_choice: null argument");
     const int st = pe::validate_gemm(*d);
     if (st != PE_OK) return st;
-    const pe::GemmChoice c = pe::choose(*d);
+    // As pe_gemm chooses for these strides, operand pointers taken as
+    // 16-byte aligned (the split is the same for every layout).
+    const int vec = d->dtype == PE_F32 ? 4 : 8;
+    const int al = pe::classify(d->M, d->K, d->a_ms, d->a_ks, d->a_bstride, d->nbatch, nullptr, vec);
+    const int bl = pe::classify(d->N, d->K, d->b_ns, d->b_ks, d->b_bstride, d->nbatch, nullptr, vec);
+    const bool dl = d->tile != 192 && pe::gemm_dl_eligible(d->dtype, al, bl, d->M, d->N, d->K, d->c_ms, d->c_ns);
+    if (d->tile == 1 || (d->tile != 2 && pe::big_f16(*d, dl, al, bl) && pe::merged_batch(*d).nbatch <= 1)) {
+        info[0] = info[1] = 256;
+        info[2] = 1;
+        info[3] = d->K;
+        return PE_OK;
+    }
+    const pe::GemmChoice c = pe::choose(*d, dl, al, bl);
     info[0] = c.bm;
     info[1] = c.bn;
     info[2] = c.nsplit;

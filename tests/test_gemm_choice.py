@@ -41,7 +41,7 @@ def test_split_counts_of_uneven_grids(shape, dtype, want):
 
 
 @pytest.mark.parametrize("shape,dtype,nb", [
-    ((1000, 1536, 777), "f32", 16),      # config 2: 768 tiles of 128x256, three per CU
+    ((1000, 1536, 777), "f32", 16),      # config 2: 1536 tiles of 128x128, four blocks per CU
     ((2048, 2048, 128), "f16", 128),     # config 3's per-head products
     ((4096, 4096, 128), "f16", 1),       # config 5.1
     ((128, 128, 128), "f32", 256),       # the GDN contraction set, 16 x 16
@@ -50,3 +50,21 @@ def test_split_counts_of_uneven_grids(shape, dtype, want):
 ])
 def test_full_grids_stay_unsplit(shape, dtype, nb):
     assert _splits(*shape, dtype=dtype, nb=nb) == 0
+
+
+def _tile(M, N, K, dtype="f32", nb=1):
+    code = launch.DT_F32 if dtype == "f32" else launch.DT_F16
+    d = launch.GemmDesc(dtype=code, batch_shape=[nb], a_bstride=[M * K], b_bstride=[K * N], c_bstride=[M * N],
+                        M=M, N=N, K=K, a_ms=1, a_ks=M, b_ks=N, b_ns=1, c_ms=N, c_ns=1,
+                        a_numel=nb * M * K, b_numel=nb * K * N, c_numel=nb * M * N)
+    info = (ctypes.c_int64 * 4)()
+    assert abi.bind().pe_gemm_choice(ctypes.byref(abi.gemm_desc(d)), info) == 0
+    return info[0], info[1]
+
+
+@pytest.mark.parametrize("shape,nb", [((1000, 1536, 777), 16), ((2048, 2048, 512), 8), ((4096, 4096, 4096), 1)])
+def test_float32_direct_load_grids_keep_128_tiles(shape, nb):
+    """MFMA-bound float32 grids with rows-contiguous operands (config 2's
+    layout) stay on 128x128 tiles: at steady clocks they beat the 256-wide
+    ones (config 2 278 against 292 us)."""
+    assert _tile(*shape, nb=nb) == (128, 128)
