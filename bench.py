@@ -184,19 +184,46 @@ def run_eager(call, sets, calls, warm_ms=50.0):
     profile summary averages); returns the number of warm-up calls."""
     import torch
 
-    call(*sets[0])
+    it = iter(range(1 << 30))
+    warm = settle(lambda: call(*sets[next(it) % len(sets)]), warm_ms)
+    for i in range(calls):
+        call(*sets[i % len(sets)])
     torch.cuda.synchronize()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
+    return warm
+
+
+def settle(fn, warm_ms=50.0):
+    """Calls fn() for at least `warm_ms` of GPU time (the clock's ramp after
+    an idle gap; see the module docstring); returns the number of calls."""
+    import torch
+
+    fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
-    call(*sets[1 % len(sets)])
+    fn()
     e1.record()
     torch.cuda.synchronize()
     warm = min(5000, int(math.ceil(warm_ms / max(e0.elapsed_time(e1), 1e-3))))
-    for i in range(warm + calls):
-        call(*sets[i % len(sets)])
-    torch.cuda.synchronize()
+    for _ in range(warm):
+        fn()
     return warm + 2
+
+
+def time_rotated(fn, sets, calls, warm_ms=50.0):
+    """GPU time (ms) per call of `calls` eager calls rotating over the sets,
+    between two events, after settle()."""
+    import torch
+
+    it = iter(range(1 << 30))
+    settle(lambda: fn(*sets[next(it) % len(sets)]), warm_ms)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(calls):
+        fn(*sets[i % len(sets)])
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / calls
 
 
 def copy_probe():
@@ -233,8 +260,7 @@ def attainable(dev):
     st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
 
     def timed(fn, reps=5):
-        for _ in range(2):
-            fn()
+        settle(fn)
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
@@ -677,8 +703,7 @@ def time_eager(fn, iters):
     events around the whole loop, so host gaps between launches count."""
     import torch
 
-    for _ in range(2):
-        fn()
+    settle(fn)
     torch.cuda.synchronize()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
@@ -696,7 +721,7 @@ def time_stage_graph(fn, iters):
     from pto_einsum import StageGraph
 
     graph = StageGraph(fn)
-    graph.replay()
+    settle(graph.replay)
     torch.cuda.synchronize()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
@@ -775,16 +800,7 @@ def time_torch_matmul(dev):
         yy = y if label == "NN" else y.t().contiguous()
         sets = replicate((x, yy), 2)
         fn = (lambda a, b: torch.matmul(a, b)) if label == "NN" else (lambda a, b: torch.matmul(a, b.t()))
-        for i in range(3):
-            fn(*sets[i % 2])
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for i in range(10):
-            fn(*sets[i % 2])
-        e1.record()
-        torch.cuda.synchronize()
-        t = e0.elapsed_time(e1) / 10
+        t = time_rotated(fn, sets, 10)
         tf = 2 * n ** 3 / t / 1e9
         out.append(dict(shape=f"{n}^3 {label}", equation="torch.matmul (float16 output)", dtype="f16",
                         us=round(t * 1e3, 1), tflops=round(tf, 1), roof="mfma",
@@ -823,16 +839,7 @@ def time_torch_thin(dev, calls=50):
         for cfg, eq, a, b, fn, out_bytes in cases:
             a, b = a.to(dev), b.to(dev)
             sets = replicate((a, b), n_sets(a.nbytes + b.nbytes + out_bytes))
-            for i in range(3):
-                fn(*sets[i % len(sets)])
-            torch.cuda.synchronize()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record()
-            for i in range(calls):
-                fn(*sets[i % len(sets)])
-            e1.record()
-            torch.cuda.synchronize()
-            t = e0.elapsed_time(e1) / calls
+            t = time_rotated(fn, sets, calls)
             tf = (2 * 16 * 1000 * 1536 * 777 if cfg == "2" else 2 * 4096 * 4096 * 128) / (t * 1e-3) / 1e12
             out.append(dict(config=cfg, equation=f"torch.{'bmm' if cfg == '2' else 'matmul'} {eq} ({a.dtype} in and out)",
                             us=round(t * 1e3, 2), tflops=round(tf, 2), operand_sets=len(sets)))
