@@ -72,3 +72,17 @@ def test_big_tile_auto_choice(eq):
     want = torch.einsum(eq, x.double(), y.double())
     assert float((got.double() - want).abs().max()) <= RTOL * float(want.abs().max())
     assert torch.equal(got, einsum(eq, x, y))
+
+
+def test_big_tile_auto_choice_below_one_round():
+    """A compute-bound float16 GEMM with 256x256 tiles for fewer CUs than the
+    device has (3072 x 2048 x 3072: 144 tiles) takes the kernel too, one
+    block per tile."""
+    g = torch.Generator().manual_seed(12)
+    x = (torch.randn(3072, 2048, generator=g) * 0.5).half().cuda()
+    y = (torch.randn(2048, 3072, generator=g) * 0.5).half().cuda()
+    print("big f16 auto: ij,jk->ik (3072, 2048) x (2048, 3072)", flush=True)
+    got = einsum("ij,jk->ik", x, y)
+    want = torch.einsum("ij,jk->ik", x.double(), y.double())
+    assert float((got.double() - want).abs().max()) <= RTOL * float(want.abs().max())
+    assert torch.equal(got, einsum("ij,jk->ik", x, y))
