@@ -8,7 +8,7 @@
 //  * four waves (2 x 2), each owning a 128 x 128 wave tile as 4 x 4 blocks
 //    of v_mfma_f32_32x32x16_f16: per 16 k a wave issues 16 MFMAs against 8
 //    fragment reads (4 for A, 4 for B), so LDS traffic per MFMA is a third
-//    below the 64 x 128 wave tile's; with k-contiguous A and B (and an even
+//    below the 64 x 128 wave tile's; with a k-contiguous A (and an even
 //    number of slabs per tile) the wave tile runs as 8 x 8 blocks of
 //    v_mfma_f32_16x16x32_f16 instead (same LDS bytes per MFMA flop; the
 //    smaller MFMA keeps a higher clock at this data's power);
@@ -29,7 +29,8 @@
 //         group g of row r sits in slot g ^ ((r / 4) % 4) (g ^ ((r / 2) % 4)
 //         for the 16x16x32 schedule);
 //   L_MN: [32 k][256 rows], 512-byte k rows of 32 groups; logical group g of
-//         k row k sits in slot g ^ (4 (k % 4)).
+//         k row k sits in slot g ^ (4 (k % 4)) (also ^ 2 ((k / 8) % 2) for
+//         the 16x16x32 schedule).
 // A lane's direct load fetches the global vector that its slot holds.
 //
 // Boundaries as in gemm_dl_kernel: rows past M / N load clamped in-bounds
@@ -138,7 +139,10 @@ struct BigOperand {
     __device__ __forceinline__ static int swz_k(int r) {
         return M16 ? ((r >> 1) & 3) : (r >> 2) & 3;
     }
-    __device__ __forceinline__ static int swz_mn(int k) { return 4 * (k & 3); }   // L_MN, by k row
+    // L_MN, by k row: 4 (k % 4); for the 16x16x32 reads (k rows 8 apart in
+    // the two 16-lane groups a transposing read serves together) also
+    // XORed with 2 ((k / 8) % 2).
+    __device__ __forceinline__ static int swz_mn(int k) { return 4 * (k & 3) ^ (M16 ? 2 * ((k >> 3) & 1) : 0); }
 
     // Issues this wave's share of one slab.  base: operand at (batch, tile
     // row 0, slab k 0); rs / ks: row and k strides; rows_left / k_left:
@@ -254,18 +258,44 @@ struct BigOperand {
         }
     }
 
-    // v_mfma_f32_16x16x32_f16 fragments (L_K): lane l reads row l % 16 and
-    // logical group l / 16 (eight k) of each 16-row block; block i adds
-    // 16 * 64 i bytes.  Per 16-lane read phase the 16 rows' groups land on
-    // 16 distinct 16-byte bank groups (rows 4 apart differ in the swizzle).
-    __device__ __forceinline__ static uint32_t lane_off16(int lane) {
-        static_assert(LAYOUT == L_K, "16x16x32 fragments are read from k-contiguous stages");
-        const int r = lane & 15;
-        return uint32_t(r * BK * 2 + 16 * ((lane >> 4) ^ swz_k(r)));
+    // v_mfma_f32_16x16x32_f16 fragments of block i (16 rows or columns).
+    //   L_K : lane l reads row l % 16, logical group l / 16 (eight k); block
+    //         i adds 16 * 64 i bytes.
+    //   L_MN: two ds_read_b64_tr_b16: lane q of 16-lane group G points at k
+    //         row 8 G + q / 4 (the second read 4 k rows on) and columns
+    //         16 i + 4 (q % 4) .. + 3, so that after the transpose lane q
+    //         holds column 16 i + q at k 8 G .. 8 G + 7; one offset per block
+    //         (the swizzle is an XOR).
+    struct LaneOff16 {
+        uint32_t o[LAYOUT == L_K ? 1 : 8];
+    };
+    __device__ __forceinline__ static LaneOff16 lane_off16(int lane) {
+        LaneOff16 x;
+        if constexpr (LAYOUT == L_K) {
+            const int r = lane & 15;
+            x.o[0] = uint32_t(r * BK * 2 + 16 * ((lane >> 4) ^ swz_k(r)));
+        } else {
+            const int q = lane & 15, k = 8 * (lane >> 4) + (q >> 2);
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                x.o[i] = uint32_t(k * ROWS * 2 + 16 * ((2 * i + ((q & 3) >> 1)) ^ swz_mn(k)) + 8 * (q & 1));
+        }
+        return x;
     }
-    __device__ __forceinline__ static f16x8 frag16(uint32_t wbase, uint32_t lo, int i) {
-        const uint32_t a = wbase + lo + uint32_t(i * 16 * BK * 2);
-        return *reinterpret_cast<const __attribute__((address_space(3))) f16x8*>(uintptr_t(a));
+    __device__ __forceinline__ static f16x8 frag16(uint32_t wbase, const LaneOff16& lo, int i) {
+        if constexpr (LAYOUT == L_K) {
+            const uint32_t a = wbase + lo.o[0] + uint32_t(i * 16 * BK * 2);
+            return *reinterpret_cast<const __attribute__((address_space(3))) f16x8*>(uintptr_t(a));
+        } else {
+            const uint32_t a = wbase + lo.o[i];
+            const i16x4 lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                reinterpret_cast<__attribute__((address_space(3))) i16x4*>(uintptr_t(a)));
+            const i16x4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                reinterpret_cast<__attribute__((address_space(3))) i16x4*>(uintptr_t(a + 4 * ROWS * 2)));
+            typedef short i16x8 __attribute__((ext_vector_type(8)));
+            const i16x8 w = {lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+            return __builtin_bit_cast(f16x8, w);
+        }
     }
 
     // Byte offset of the wave's first row within a stage.
@@ -285,7 +315,7 @@ __device__ __forceinline__ const _Float16* big_uniform(const _Float16* p) {
 
 // TAIL: K is not a whole number of 32-k slabs (the last slab of each tile
 // has a K tail); without one, the per-slab tail checks are compiled out.
-// M16 (k-contiguous A and B only): each wave's 128 x 128 tile as 8 x 8
+// M16 (k-contiguous A only): each wave's 128 x 128 tile as 8 x 8
 // blocks of v_mfma_f32_16x16x32_f16, one MFMA per block and slab (64 per
 // slab, accumulators in all 256 AGPRs), the next slab's 16 fragments read
 // into a second register set during the slab's MFMAs; the same loads, LDS
@@ -433,10 +463,11 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_big_kernel(GemmArgs g) {
     tail_fix(0, 0);
 
     if constexpr (M16) {
-        static_assert(AL == L_K && BL == L_K, "16x16x32 schedule: k-contiguous operands");
+        static_assert(AL == L_K, "16x16x32 schedule: k-contiguous A");
         uint32_t cstage = 0;  // byte offset of the stage being computed
         int gs = 0;           // slabs computed
-        const uint32_t loa16 = OA::lane_off16(lane), lob16 = OB::lane_off16(lane);
+        const typename OA::LaneOff16 loa16 = OA::lane_off16(lane);
+        const typename OB::LaneOff16 lob16 = OB::lane_off16(lane);
         f16x8 xa[8], xb[8], ya[8], yb[8];
         // Fragment reads in the order the MFMAs use them (A 0, B 0..7, A 1..7).
         auto read16 = [&](f16x8 (&fa)[8], f16x8 (&fb)[8], uint32_t a, uint32_t b, int u) {

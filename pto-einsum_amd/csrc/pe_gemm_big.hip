@@ -7,14 +7,15 @@
 
 namespace pe {
 
-// M16: the 16x16x32 schedule, for k-contiguous A and B with an even number
-// of 32-k slabs per tile.
+// M16: the 16x16x32 schedule, for a k-contiguous A with an even number of
+// 32-k slabs per tile.
 template <bool TAIL>
 static const void* big_kernel_t(int al, int bl, bool m16) {
     if (al == L_K)
         return bl == L_K ? (m16 ? reinterpret_cast<const void*>(&gemm_big_kernel<L_K, L_K, TAIL, true>)
                                 : reinterpret_cast<const void*>(&gemm_big_kernel<L_K, L_K, TAIL, false>))
-                         : reinterpret_cast<const void*>(&gemm_big_kernel<L_K, L_MN, TAIL, false>);
+                         : (m16 ? reinterpret_cast<const void*>(&gemm_big_kernel<L_K, L_MN, TAIL, true>)
+                                : reinterpret_cast<const void*>(&gemm_big_kernel<L_K, L_MN, TAIL, false>));
     return bl == L_K ? reinterpret_cast<const void*>(&gemm_big_kernel<L_MN, L_K, TAIL, false>)
                      : reinterpret_cast<const void*>(&gemm_big_kernel<L_MN, L_MN, TAIL, false>);
 }
@@ -49,7 +50,7 @@ hipError_t launch_gemm_big(int al, int bl, const GemmArgs& g, hipStream_t s) {
     const uint32_t cap = uint32_t(cu_count()) * uint32_t(resident);
     if (a.grid > cap) a.grid = cap;
     void* args[] = {&a};
-    const bool m16 = al == L_K && bl == L_K && ((a.K + 31) / 32) % 2 == 0;
+    const bool m16 = al == L_K && ((a.K + 31) / 32) % 2 == 0;
     return hipLaunchKernel(big_kernel(al, bl, a.K % 32 != 0, m16), dim3(a.grid), dim3(kGemmThreads), args, 0, s);
 }
 
