@@ -7,7 +7,7 @@ import pytest
 import torch
 
 from pto_einsum import einsum, launch
-from test_gpu_components import _gemm_direct
+from test_gpu_components import _gemm_direct, _gemm_out_strides
 
 pytestmark = pytest.mark.gpu
 
@@ -86,3 +86,22 @@ def test_big_tile_auto_choice_below_one_round():
     want = torch.einsum("ij,jk->ik", x.double(), y.double())
     assert float((got.double() - want).abs().max()) <= RTOL * float(want.abs().max())
     assert torch.equal(got, einsum("ij,jk->ik", x, y))
+
+
+@pytest.mark.parametrize("out", ["cols", "pitch"])
+@pytest.mark.parametrize("layout_a,layout_b,K", [("k", "k", 64), ("k", "mn", 104), ("mn", "mn", 96),
+                                                 ("mn", "k", 64)], ids=lambda v: str(v))
+def test_big_tile_output_strides(layout_a, layout_b, K, out):
+    """The 256x256 kernel's output addressing away from contiguous rows: a
+    column-major output and rows with a pitch that is not a whole number of
+    16-byte vectors, with partial tiles in M and N, on both of its schedules
+    (k-contiguous A with an even slab count: 16x16x32 blocks; otherwise
+    32x32x16)."""
+    nbatch, M, N = 2, 520, 264
+    print(f"big f16 out={out}: {layout_a}/{layout_b} b={nbatch} {M}x{N}x{K}", flush=True)
+    A, B, a, b, a_ms, a_ks, b_ks, b_ns = _operands(nbatch, M, N, K, layout_a, layout_b, 31 + K)
+    got, gaps = _gemm_out_strides(A, B, a, b, a_ms, a_ks, b_ks, b_ns, launch.DT_F16, 1, out)
+    want = torch.bmm(A.double(), B.double())
+    assert float((got.double() - want).abs().max()) <= RTOL * float(want.abs().max())
+    if gaps is not None:
+        assert bool(torch.isnan(gaps).all())

@@ -260,6 +260,54 @@ def test_gemm_tiles_direct(tile, dtype, M, N, K, layout, split_k):
     assert float(np.abs(got.numpy() - want).max()) <= rtol * scale
 
 
+def _gemm_out_strides(A, B, a, b, a_ms, a_ks, b_ks, b_ns, dtype_code, tile, out, split_k=0):
+    """pe_gemm with the output stored column-major ("cols": c_ms = 1, c_ns =
+    M) or row-major with a row pitch past N ("pitch": c_ms = N + 5, whose
+    rows are not whole 16-byte vectors); returns the product as [b][M][N]
+    and the elements between the rows, which must stay untouched (NaN)."""
+    nb, M, K = A.shape
+    N = B.shape[2]
+    c_ms, c_ns, c_bs = (1, M, M * N) if out == "cols" else (N + 5, 1, M * (N + 5))
+    c_numel = nb * c_bs
+    d = launch.GemmDesc(dtype=dtype_code, batch_shape=[nb], a_bstride=[a.numel() // nb],
+                        b_bstride=[b.numel() // nb], c_bstride=[c_bs], M=M, N=N, K=K, a_ms=a_ms, a_ks=a_ks,
+                        b_ks=b_ks, b_ns=b_ns, c_ms=c_ms, c_ns=c_ns, a_numel=a.numel(), b_numel=b.numel(),
+                        c_numel=c_numel, split_k=split_k, tile=tile)
+    lib = abi.bind()
+    cd = abi.gemm_desc(d)
+    ws_bytes = lib.pe_gemm_workspace_bytes(ctypes.byref(cd))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device="cuda")
+    c = torch.full((c_numel,), float("nan"), dtype=torch.float32, device="cuda")
+    rc = lib.pe_gemm(ctypes.byref(cd), _ptr(a), _ptr(b), _ptr(c), _ptr(ws), ws_bytes, _stream())
+    assert rc == 0, runtime.last_error()
+    got = torch.as_strided(c, (nb, M, N), (c_bs, c_ms, c_ns)).cpu()
+    gaps = None if out == "cols" else torch.as_strided(c, (nb, M, 5), (c_bs, c_ms, 1), N).cpu()
+    return got, gaps
+
+
+@pytest.mark.parametrize("out", ["cols", "pitch"])
+@pytest.mark.parametrize("tile,dtype", [(64, torch.float32), (128, torch.float32), (256, torch.float32),
+                                        (128, torch.float16), (256, torch.float16)])
+@pytest.mark.parametrize("split_k", [0, 3])
+def test_gemm_tiles_output_strides(tile, dtype, split_k, out):
+    """Tile shapes with the output column-major or with a row pitch that is
+    not a whole number of 16-byte vectors (gaps between rows untouched),
+    partial tiles in M and N, with and without split-K."""
+    nbatch, M, N, K = 2, 304, 200, 80
+    g = torch.Generator().manual_seed(tile + split_k + len(out))
+    A = torch.randn(nbatch, M, K, generator=g).to(dtype)
+    B = torch.randn(nbatch, K, N, generator=g).to(dtype)
+    a_buf, b_buf = A.contiguous(), B.transpose(1, 2).contiguous()
+    code = launch.DT_F32 if dtype == torch.float32 else launch.DT_F16
+    got, gaps = _gemm_out_strides(A, B, a_buf.reshape(-1).cuda(), b_buf.reshape(-1).cuda(), K, 1, 1, K, code,
+                                  tile, out, split_k=split_k)
+    want = torch.bmm(A.double(), B.double())
+    rtol = 1e-4 if dtype == torch.float32 else 2e-3
+    assert float((got.double() - want).abs().max()) <= rtol * float(want.abs().max())
+    if gaps is not None:
+        assert bool(torch.isnan(gaps).all())
+
+
 @pytest.mark.parametrize("c_ms", [2_000_003, 2_200_001], ids=["dl-near-limit", "staged-beyond-limit"])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16], ids=["f32", "f16"])
 def test_gemm_large_output_row_stride(c_ms, dtype):

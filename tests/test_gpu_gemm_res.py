@@ -84,3 +84,34 @@ def test_public_einsum_shapes_that_take_it(eq, s0, s1, dt):
     want = torch.einsum(eq, x.double(), y.double())
     bound = torch.einsum(eq, x.double().abs(), y.double().abs())
     assert bool(((got - want).abs() <= 1e-5 * bound + 1e-6).all())
+
+
+@pytest.mark.parametrize("out", ["cols", "pitch"])
+@pytest.mark.parametrize("dt,al,bl,K", [("f16", "k", "mn", 120), ("f16", "mn", "k", 104),
+                                        ("f32", "k", "k", 124), ("f32", "mn", "mn", 116)])
+def test_short_k_output_strides(dt, al, bl, K, out):
+    """The short-K kernel's stores away from contiguous rows: a column-major
+    output, and rows with a pitch (N + 5) that is not a whole number of
+    16-byte vectors, whose gaps stay untouched; partial tiles in M and N."""
+    nb, M, N = 2, 200, 136
+    g = torch.Generator().manual_seed(K * 3 + len(out))
+    tdt = torch.float16 if dt == "f16" else torch.float32
+    A = (torch.randn(nb, M, K, generator=g) / 8).to(tdt)
+    B = (torch.randn(nb, K, N, generator=g) / 8).to(tdt)
+    a_buf, a_ms, a_ks = (A.transpose(1, 2).contiguous(), 1, M) if al == "mn" else (A.contiguous(), K, 1)
+    b_buf, b_ks, b_ns = (B.contiguous(), N, 1) if bl == "mn" else (B.transpose(1, 2).contiguous(), 1, K)
+    c_ms, c_ns, c_bs = (1, M, M * N) if out == "cols" else (N + 5, 1, M * (N + 5))
+    d = launch.GemmDesc(dtype=launch.DT_F16 if dt == "f16" else launch.DT_F32, batch_shape=[nb],
+                        a_bstride=[M * K], b_bstride=[K * N], c_bstride=[c_bs], M=M, N=N, K=K, a_ms=a_ms,
+                        a_ks=a_ks, b_ks=b_ks, b_ns=b_ns, c_ms=c_ms, c_ns=c_ns, a_numel=nb * M * K,
+                        b_numel=nb * K * N, c_numel=nb * c_bs, tile=2)
+    lib = abi.bind()
+    cd = abi.gemm_desc(d)
+    a, b = a_buf.reshape(-1).cuda(), b_buf.reshape(-1).cuda()
+    c = torch.full((nb * c_bs,), float("nan"), device="cuda")
+    rc = lib.pe_gemm(ctypes.byref(cd), _ptr(a), _ptr(b), _ptr(c), None, 0,
+                     ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert rc == 0, runtime.last_error()
+    _check(torch.as_strided(c, (nb, M, N), (c_bs, c_ms, c_ns)), A, B)
+    if out == "pitch":
+        assert bool(torch.isnan(torch.as_strided(c, (nb, M, 5), (c_bs, c_ms, 1), N)).all())
