@@ -82,9 +82,9 @@ typedef struct pe_gemm_desc {
     int32_t tile;                       /* 0 = choose; 64 or 128 (square); 256 = 256x128
                                            (M >= N) or 128x256; 192 (float32 only) =
                                            192x128 (M >= N) or 128x192; 1 = the float16
-                                           256x256 kernel; 2 = the short-K kernel (128x128,
-                                           all of K resident in LDS: float16 K in (96, 128],
-                                           float32 K in (112, 128]) */
+                                           256x256 kernel; 2 = the short-K kernel (all of K
+                                           resident in LDS: float16 K in (96, 128] on 64x128
+                                           tiles, float32 K in (112, 128] on 128x128) */
     int64_t batch_shape[PE_MAX_DIMS];
     int64_t a_bstride[PE_MAX_DIMS], b_bstride[PE_MAX_DIMS], c_bstride[PE_MAX_DIMS];
     int64_t M, N, K;

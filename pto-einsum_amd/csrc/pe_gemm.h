@@ -116,12 +116,15 @@ hipError_t launch_gemm_dl(int dtype, int bm, int bn, int minb, int al, int bl, b
                           hipStream_t s);
 hipError_t launch_gemm_f16(int bm, int bn, int alayout, int blayout, int persist, const GemmArgs& g,
                            hipStream_t s);
-// Short-K kernel (gemm_res_kernel in pe_gemm_dl.h): 128x128 tiles with every
-// k slab resident in LDS (float16: four 32-k slabs, K in (96, 128]; float32:
-// eight 16-k slabs, K in (112, 128]), one block per tile, operands L_MN or
-// L_K under the gemm_dl_eligible conditions, no split.
-// gemm_res_resident: resident blocks per CU (0 when it spilled).
+// Short-K kernel (gemm_res_kernel in pe_gemm_dl.h): every k slab resident in
+// LDS (float16: 64x128 tiles, four 32-k slabs, K in (96, 128]; float32:
+// 128x128 tiles, eight 16-k slabs, K in (112, 128]), one block per tile,
+// operands L_MN or L_K under the gemm_dl_eligible conditions, no split.
+// gemm_res_resident: resident blocks per CU (0 when it spilled);
+// gemm_res_tile_m / _n: its tile rows (of A) and columns (rows of B).
 int gemm_res_resident(int dtype, int alayout, int blayout);
+int gemm_res_tile_m(int dtype);
+int gemm_res_tile_n(int dtype);
 hipError_t launch_gemm_res(int dtype, int alayout, int blayout, const GemmArgs& g, hipStream_t s);
 // k-split kernel (pe_gemm_ks.h): float32 32x32 or 64x64 tiles, float16 64x64
 // tiles (`tile`), one block per tile and batch, the block's waves splitting

@@ -59,13 +59,16 @@
 #endif
 
 // float16 products with K in (96, 128] take the short-K kernel (all of K
-// resident in LDS) on grids of at most this many 128x128 tiles per CU.
-// Measured on MI355X against the two-stage direct-load kernel (float32
-// output, cold operands and outputs): 4096^2 x 128 (config 5.1, 4 tiles per
-// CU) 18.0 -> 16.2 us, 4096 x 8192 x 128 (8) 31.0 -> 26.9, 8192^2 x 128 (16)
-// 51.6 -> 48.2, 8192 x 16384 x 128 (32) 117.9 -> 92.8; config 3 (128 tiles
-// per CU, its 2.15 GB output the bound) 403-412 -> 439 us, so it keeps the
-// two-stage kernel, whose four blocks per CU keep more stores in flight.
+// resident in LDS) on grids of at most this many 128x128 tiles per CU (the
+// kernel itself runs 64x128 tiles, pe_gemm_dl.hip).  Measured on MI355X
+// against the two-stage direct-load kernel (float32 output, cold operands and
+// outputs), first with 128x128 short-K tiles: 4096^2 x 128 (config 5.1, 4
+// tiles per CU) 18.0 -> 16.2 us, 4096 x 8192 x 128 (8) 31.0 -> 26.9, 8192^2
+// x 128 (16) 51.6 -> 48.2, 8192 x 16384 x 128 (32) 117.9 -> 92.8; config 3
+// (128 tiles per CU, its 2.15 GB output the bound) 403-412 -> 439 us with
+// 128x128 and 482 us with 64x128 short-K tiles, and 4 x 8192^2 x 128 (64
+// per CU) 184-185 -> 188 us, so those keep the two-stage kernel, whose four
+// blocks per CU keep more stores in flight.
 // The float32 variant (eight 16-k slabs, one block per CU; pe_gemm_desc.tile
 // = 2) is not chosen automatically: on the GDN 16x16 contractions (256 x
 // 128^3, one 128x128 tile per CU) it took 20.8-22.6 us against 18.9-19.6 us
@@ -511,6 +514,17 @@ bool dl_off32(const pe_gemm_desc& d) {
     return span_ok(d.a_ms, d.a_ks) && span_ok(d.b_ns, d.b_ks);
 }
 
+// float16 products with K in (96, 128] (four 32-k slabs) that the tile
+// choice leaves unsplit on 128x128 tiles, at most
+// PE_GEMM_RES_MAX_TILES_PER_CU of those per CU: the short-K kernel, all of K
+// in flight at once.
+bool res_auto(const pe_gemm_desc& d, const GemmChoice& ch, bool dl, int al, int bl) {
+    return PE_GEMM_RES && dl && d.dtype == PE_F16 && d.split_k == 0 && d.tile == 0 && ch.nsplit == 1 &&
+           ch.bm == 128 && ch.bn == 128 && d.K > 96 && d.K <= 128 &&
+           batch_total(d) * ceil_div(d.M, 128) * ceil_div(d.N, 128) <= PE_GEMM_RES_MAX_TILES_PER_CU * cu_count() &&
+           gemm_res_resident(d.dtype, al, bl) >= 1;
+}
+
 // Launch of the short-K kernel (gemm_res_kernel) for descriptor d.
 hipError_t launch_res(const pe_gemm_desc& d, const void* a, const void* b, float* c, int64_t nb, int al, int bl,
                       hipStream_t s) {
@@ -520,8 +534,8 @@ hipError_t launch_res(const pe_gemm_desc& d, const void* a, const void* b, float
     g.M = int32_t(d.M); g.N = int32_t(d.N); g.K = int32_t(d.K);
     g.nsplit = 1;
     g.k_per_split = int32_t(d.K);
-    g.tiles_m = int32_t(ceil_div(d.M, 128));
-    g.tiles_n = int32_t(ceil_div(d.N, 128));
+    g.tiles_m = int32_t(ceil_div(d.M, gemm_res_tile_m(d.dtype)));
+    g.tiles_n = int32_t(ceil_div(d.N, gemm_res_tile_n(d.dtype)));
     g.tiles_per_batch = uint32_t(g.tiles_m) * uint32_t(g.tiles_n);
     g.nbatch_total = uint32_t(nb);
     g.total_blocks = g.tiles_per_batch * g.nbatch_total;
@@ -619,6 +633,13 @@ extern "C" int pe_gemm_choice(const pe_gemm_desc* d, int64_t* info) {
         return PE_OK;
     }
     const pe::GemmChoice c = pe::choose(*d, dl, al, bl);
+    if (d->tile == 2 || pe::res_auto(*d, c, dl, al, bl)) {
+        info[0] = pe::gemm_res_tile_m(d->dtype);
+        info[1] = pe::gemm_res_tile_n(d->dtype);
+        info[2] = 1;
+        info[3] = d->K;
+        return PE_OK;
+    }
     info[0] = c.bm;
     info[1] = c.bn;
     info[2] = c.nsplit;
@@ -737,12 +758,7 @@ extern "C" int pe_gemm(const pe_gemm_desc* d, const void* a, const void* b, floa
     // 4096 22.6 against 26.4, 1664 x 2304 x 3072 with 3.7 tiles per CU 48.8
     // against 60.1).
     const int64_t cus = cu_count();
-    // float16 products with K in (96, 128] (four 32-k slabs), unsplit, on
-    // 128x128 tiles: the short-K kernel, all of K in flight at once.
-    if (PE_GEMM_RES && dl && d->dtype == PE_F16 && d->split_k == 0 && d->tile == 0 && ch.nsplit == 1 &&
-        ch.bm == 128 && ch.bn == 128 && d->K > 96 && d->K <= 128 &&
-        nb * ceil_div(d->M, 128) * ceil_div(d->N, 128) <= PE_GEMM_RES_MAX_TILES_PER_CU * cus &&
-        gemm_res_resident(d->dtype, al, bl) >= 1) {
+    if (res_auto(*d, ch, dl, al, bl)) {
         PE_CHECK_HIP(launch_res(*d, a, b, c, nb, al, bl, s));
         return PE_OK;
     }

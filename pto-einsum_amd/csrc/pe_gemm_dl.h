@@ -347,7 +347,11 @@ struct DlOperand {
             v[st % 2] = *reinterpret_cast<const f16x8*>(stage + lo.o[st] + i * 32 * BK);
         } else {
             const int C = wrow0 / 8 + 4 * i;
-            const T* p = stage + lo.o[(C >> 2) & 1] + 8 * (C & ~7) + 16 * st * ROWS;
+            // A select, not an index: with 32-row wave tiles the parity
+            // depends on the wave, and an indexed lane_off array would be
+            // kept in scratch memory.
+            const int lo_par = ((C >> 2) & 1) ? lo.o[1] : lo.o[0];
+            const T* p = stage + lo_par + 8 * (C & ~7) + 16 * st * ROWS;
             const i16x4 lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                 (__attribute__((address_space(3))) i16x4*)(p));
             const i16x4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -587,9 +591,11 @@ __global__ __launch_bounds__(kGemmThreads, MINB) void gemm_dl_kernel(GemmArgs g)
 // slab's MFMAs take far less than a load's latency (float16, 128 x 128
 // tiles: 8 MFMAs of 32 cycles per wave and slab) its NS slabs cost NS load
 // latencies in a row; here they cost one.  LDS: NS x (BM + BN) x 64 bytes
-// (64 KB for 128 x 128 float16 tiles and K = 128, two blocks per CU).
-// Measured on MI355X: config 5.1 (tn,sn->ts, 4096^2 x 128 float16, float32
-// out) with its output stores removed ran 9.5 us of its 17.8; float32 short K
+// (48 KB for the 64 x 128 float16 tiles at K = 128, three blocks per CU; a
+// block keeps them until its output stores complete, and the other resident
+// blocks load and multiply meanwhile).  Measured on MI355X: config 5.1
+// (tn,sn->ts, 4096^2 x 128 float16, float32 out) with its output stores
+// removed ran 9.5 us of its 17.8 (two-stage kernel); float32 short K
 // (the GDN chunk products, K = 128 in eight slabs) ran slower than the
 // two-stage kernel both as 128 x 128 tiles at one block per CU (22 against
 // 20 us at 256 x 128^3, 68 against 54 us at 1024 x 128^3) and as 64 x 64

@@ -90,20 +90,44 @@ hipError_t launch_gemm_dl(int dtype, int bm, int bn, int minb, int al, int bl, b
     return hipLaunchKernel(dl_kernel(dtype, bm, bn, minb, al, bl), dim3(a.grid), dim3(kGemmThreads), args, 0, s);
 }
 
-// Short-K all-resident kernel (gemm_res_kernel): 128x128 tiles with every k
-// slab of K resident in LDS.  float16: four 32-k slabs (K in (96, 128]), two
-// blocks per CU; float32: eight 16-k slabs (K in (112, 128]), one block per CU.
-template <typename E, int NS, int MINB>
+// Short-K all-resident kernel (gemm_res_kernel), every k slab of K resident
+// in LDS.  float16: 64x128 tiles (A rows x B rows), four 32-k slabs (K in
+// (96, 128]), 48 KB of LDS, three blocks per CU; float32: 128x128 tiles,
+// eight 16-k slabs (K in (112, 128]), one block per CU.  A block holds its
+// registers and LDS until its output stores have completed, so the number
+// of resident blocks sets how much of one block's store drain overlaps the
+// loads and MFMAs of others.  float16 on one MI355X (float32 output, cold
+// operands and outputs), 64x128 against 128x128 tiles at two blocks per CU:
+// 4096^2 x 128 (config 5.1) 15.8-16.0 -> 14.4-14.5 us, 2048^2 x 128 8.2 ->
+// 7.8, 4096 x 8192 x 128 27.2-27.4 -> 25.9, 8192^2 x 128 50.0-50.3 -> 50.5,
+// 8192 x 16384 x 128 100.1-101.6 -> 96.4, K = 112 at 4096^2 16.7 -> 16.2;
+// 64x64 tiles at five blocks per CU: 15.4, 7.9, 27.6, 54.7, 102.2 and
+// 15.1 us.
+#ifndef PE_GEMM_RES_F16_BM
+#define PE_GEMM_RES_F16_BM 64
+#endif
+#ifndef PE_GEMM_RES_F16_BN
+#define PE_GEMM_RES_F16_BN 128
+#endif
+#ifndef PE_GEMM_RES_F16_MINB
+#define PE_GEMM_RES_F16_MINB 3
+#endif
+template <typename E, int BM, int BN, int NS, int MINB>
 static const void* res_kernel_t(int al, int bl) {
     if (al == L_MN)
-        return bl == L_MN ? reinterpret_cast<const void*>(&gemm_res_kernel<E, 128, 128, L_MN, L_MN, NS, MINB>)
-                          : reinterpret_cast<const void*>(&gemm_res_kernel<E, 128, 128, L_MN, L_K, NS, MINB>);
-    return bl == L_MN ? reinterpret_cast<const void*>(&gemm_res_kernel<E, 128, 128, L_K, L_MN, NS, MINB>)
-                      : reinterpret_cast<const void*>(&gemm_res_kernel<E, 128, 128, L_K, L_K, NS, MINB>);
+        return bl == L_MN ? reinterpret_cast<const void*>(&gemm_res_kernel<E, BM, BN, L_MN, L_MN, NS, MINB>)
+                          : reinterpret_cast<const void*>(&gemm_res_kernel<E, BM, BN, L_MN, L_K, NS, MINB>);
+    return bl == L_MN ? reinterpret_cast<const void*>(&gemm_res_kernel<E, BM, BN, L_K, L_MN, NS, MINB>)
+                      : reinterpret_cast<const void*>(&gemm_res_kernel<E, BM, BN, L_K, L_K, NS, MINB>);
 }
 static const void* res_kernel(int dtype, int al, int bl) {
-    return dtype == PE_F32 ? res_kernel_t<F32, 8, 1>(al, bl) : res_kernel_t<F16, 4, 2>(al, bl);
+    return dtype == PE_F32 ? res_kernel_t<F32, 128, 128, 8, 1>(al, bl)
+                           : res_kernel_t<F16, PE_GEMM_RES_F16_BM, PE_GEMM_RES_F16_BN, 4, PE_GEMM_RES_F16_MINB>(al, bl);
 }
+
+// Tile rows and columns of the short-K kernel for dtype.
+int gemm_res_tile_m(int dtype) { return dtype == PE_F32 ? 128 : PE_GEMM_RES_F16_BM; }
+int gemm_res_tile_n(int dtype) { return dtype == PE_F32 ? 128 : PE_GEMM_RES_F16_BN; }
 
 int gemm_res_resident(int dtype, int al, int bl) {
     static int cache[2][4] = {{-1, -1, -1, -1}, {-1, -1, -1, -1}};

@@ -68,3 +68,17 @@ def test_float32_direct_load_grids_keep_128_tiles(shape, nb):
     layout) stay on 128x128 tiles: at steady clocks they beat the 256-wide
     ones (config 2 278 against 292 us)."""
     assert _tile(*shape, nb=nb) == (128, 128)
+
+
+@pytest.mark.parametrize("dtype,K,want", [("f16", 128, [64, 128, 1, 128]), ("f32", 120, [128, 128, 1, 120])])
+def test_short_k_tile_reported(dtype, K, want):
+    """pe_gemm_desc.tile = 2 (the short-K kernel) is reported with that
+    kernel's tile: 64x128 for float16, 128x128 for float32, unsplit."""
+    M = N = 1024
+    code = launch.DT_F32 if dtype == "f32" else launch.DT_F16
+    d = launch.GemmDesc(dtype=code, batch_shape=[1], a_bstride=[M * K], b_bstride=[K * N], c_bstride=[M * N],
+                        M=M, N=N, K=K, a_ms=K, a_ks=1, b_ks=1, b_ns=K, c_ms=N, c_ns=1,
+                        a_numel=M * K, b_numel=K * N, c_numel=M * N, tile=2)
+    info = (ctypes.c_int64 * 4)()
+    assert abi.bind().pe_gemm_choice(ctypes.byref(abi.gemm_desc(d)), info) == 0
+    assert list(info) == want

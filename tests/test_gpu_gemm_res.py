@@ -1,11 +1,12 @@
-"""The short-K GEMM kernel (every k slab of a 128x128 tile resident in LDS,
-all loads issued up front: float16 with K in (96, 128], float32 with K in
-(112, 128]; forced with pe_gemm_desc.tile = 2 at sizes the automatic choice
-sends elsewhere): every operand layout pairing, K tails inside the last slab,
-partial tiles in M and N and batches, against a float64 reference, with
-run-to-run equality (the reference checks its batched matmul the same way,
-test_einsum.py:244-364); and config 5.1 and a config-3-shaped product
-through the public einsum, which choose the float16 variant."""
+"""The short-K GEMM kernel (every k slab of a tile resident in LDS, all
+loads issued up front: float16 with K in (96, 128] on 64x128 tiles, float32
+with K in (112, 128] on 128x128 tiles; forced with pe_gemm_desc.tile = 2 at
+sizes the automatic choice sends elsewhere): every operand layout pairing, K
+tails inside the last slab, partial tiles in M and N and batches, against a
+float64 reference, with run-to-run equality (the reference checks its
+batched matmul the same way, test_einsum.py:244-364); config 5.1 and a
+config-3-shaped product through the public einsum, which choose the float16
+variant; and the tile that pe_gemm_choice reports for config 5.1."""
 import ctypes
 
 import pytest
@@ -115,3 +116,17 @@ def test_short_k_output_strides(dt, al, bl, K, out):
     _check(torch.as_strided(c, (nb, M, N), (c_bs, c_ms, c_ns)), A, B)
     if out == "pitch":
         assert bool(torch.isnan(torch.as_strided(c, (nb, M, 5), (c_bs, c_ms, 1), N)).all())
+
+
+def test_choice_reports_the_short_k_tile():
+    """Config 5.1's product (4096^2 x 128 float16, both operands k
+    contiguous) takes the short-K kernel by itself, and pe_gemm_choice says
+    so with its 64x128 tile."""
+    M = N = 4096
+    K = 128
+    d = launch.GemmDesc(dtype=launch.DT_F16, batch_shape=[1], a_bstride=[M * K], b_bstride=[K * N],
+                        c_bstride=[M * N], M=M, N=N, K=K, a_ms=K, a_ks=1, b_ks=1, b_ns=K, c_ms=N, c_ns=1,
+                        a_numel=M * K, b_numel=K * N, c_numel=M * N)
+    info = (ctypes.c_int64 * 4)()
+    assert abi.bind().pe_gemm_choice(ctypes.byref(abi.gemm_desc(d)), info) == 0
+    assert list(info) == [64, 128, 1, 128]
