@@ -22,6 +22,7 @@
 #include "pe_common.h"
 
 #include <algorithm>
+#include <type_traits>
 #include <vector>
 
 // Blocks per CU of the grid-stride stream and vectors per thread per
@@ -36,6 +37,14 @@
 #endif
 #ifndef PE_PRODUCT_UNROLL
 #define PE_PRODUCT_UNROLL 1
+#endif
+// Products with outer axes (a broadcast operand: configs 4b, 5.R) issue the
+// next iteration's loads before this iteration's stores.  One MI355X, same
+// box, cold operands and outputs: 5.R 41.7-42.2 -> 36.8-37.2 us, 4b
+// 149.0-150.5 -> 146.1-147.2 us; flat products (4a, 5.2) measured 1-2 %
+// slower that way and keep one iteration's loads and stores in turn.
+#ifndef PE_PRODUCT_PIPE
+#define PE_PRODUCT_PIPE 1
 #endif
 #ifndef PE_PRODUCT_VEC_F32
 #define PE_PRODUCT_VEC_F32 4
@@ -155,9 +164,32 @@ __device__ __forceinline__ void store_out(float* out, const float (&r)[VEC], boo
     }
 }
 
+// As store_out with the store flavour fixed at compile time: the compiler's
+// own non-temporal store (no branch for it to merge), which its
+// memory-counter waits then count (an assembly store is invisible to them).
+template <int VEC, bool NT>
+__device__ __forceinline__ void store_out_fixed(float* out, const float (&r)[VEC]) {
+    if constexpr (VEC == 4 || VEC == 8) {
+#pragma unroll
+        for (int h = 0; h < VEC / 4; ++h) {
+            const f32x4 v = {r[4 * h], r[4 * h + 1], r[4 * h + 2], r[4 * h + 3]};
+            f32x4* q = reinterpret_cast<f32x4*>(out) + h;
+            if constexpr (NT) __builtin_nontemporal_store(v, q);
+            else *q = v;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) {
+            if constexpr (NT) __builtin_nontemporal_store(r[i], out + i);
+            else out[i] = r[i];
+        }
+    }
+}
+
 // One launch streams all output vectors.  UNROLL vectors per thread per
 // iteration: all loads are issued before any store so several 16-byte loads
-// are in flight per lane.
+// are in flight per lane; with outer axes (PE_PRODUCT_PIPE) the next
+// iteration's loads go out before this iteration's stores as well.
 template <typename E, int VEC, int B_MODE, bool ADD_ZERO, bool HAS_OUTER, int UNROLL>
 __global__ __launch_bounds__(kThreads) void product_kernel(ProductArgs p) {
     using T = typename E::T;
@@ -166,14 +198,22 @@ __global__ __launch_bounds__(kThreads) void product_kernel(ProductArgs p) {
     float* __restrict__ out = p.out;
     const uint32_t stride = gridDim.x * kThreads;
     uint32_t v = blockIdx.x * kThreads + threadIdx.x;
-    for (; v < p.nvec; v += stride * UNROLL) {
-        float ra[UNROLL][VEC], rb[UNROLL][VEC];
-        bool live[UNROLL];
+    // Loads of the UNROLL vectors v0 + u * stride into (xa, xb); CHECK:
+    // vectors past the end are skipped (lv false), else their index is
+    // clamped to the last vector (loaded, never stored): no branch around a
+    // load, so the compiler's memory-counter waits stay exact.
+    auto fetch = [&](auto check, uint32_t v0, float (&xa)[UNROLL][VEC], float (&xb)[UNROLL][VEC],
+                     bool (&lv)[UNROLL]) {
+        constexpr bool CHECK = decltype(check)::value;
 #pragma unroll
         for (int u = 0; u < UNROLL; ++u) {
-            uint32_t vv = v + u * stride;
-            live[u] = vv < p.nvec;
-            if (!live[u]) continue;
+            uint32_t vv = v0 + u * stride;
+            lv[u] = vv < p.nvec;
+            if (CHECK) {
+                if (!lv[u]) continue;
+            } else {
+                vv = min(vv, p.nvec - 1);
+            }
             int64_t aoff, boff;
             if constexpr (HAS_OUTER) {
                 uint32_t row, colv;
@@ -205,25 +245,90 @@ __global__ __launch_bounds__(kThreads) void product_kernel(ProductArgs p) {
                 boff = int64_t(vv) * VEC * p.b_inner;
             }
             if constexpr (VEC > 1 && !HAS_OUTER) {
-                load_stream<E, VEC>(a + aoff, ra[u]);
+                load_stream<E, VEC>(a + aoff, xa[u]);
             } else if constexpr (VEC > 1) {
-                VecLoad<E, VEC>::load(a + aoff, ra[u]);
+                VecLoad<E, VEC>::load(a + aoff, xa[u]);
             } else {
-                ra[u][0] = E::to_f32(a[aoff]);
+                xa[u][0] = E::to_f32(a[aoff]);
             }
-            load_b<E, VEC, B_MODE>(b, boff, p.b_inner, rb[u]);
+            load_b<E, VEC, B_MODE>(b, boff, p.b_inner, xb[u]);
         }
+    };
+    // Products and stores of the vectors fetched for v0 (CHECK: live ones;
+    // nt: non-temporal stores, a run-time flag or a compile-time constant).
+    auto finish = [&](auto check, auto nt, uint32_t v0, const float (&xa)[UNROLL][VEC],
+                      const float (&xb)[UNROLL][VEC], const bool (&lv)[UNROLL]) {
+        constexpr bool CHECK = decltype(check)::value;
 #pragma unroll
         for (int u = 0; u < UNROLL; ++u) {
-            if (!live[u]) continue;
+            if (CHECK && !lv[u]) continue;
             float r[VEC];
 #pragma unroll
             for (int i = 0; i < VEC; ++i) {
-                float prod = ra[u][i] * rb[u][i];
+                float prod = xa[u][i] * xb[u][i];
                 r[i] = ADD_ZERO ? 0.0f + prod : prod;
             }
-            store_out<VEC>(out + int64_t(v + u * stride) * VEC, r, p.nt != 0);
+            if constexpr (std::is_same_v<decltype(nt), bool>)
+                store_out<VEC>(out + int64_t(v0 + u * stride) * VEC, r, nt);
+            else
+                store_out_fixed<VEC, decltype(nt)::value>(out + int64_t(v0 + u * stride) * VEC, r);
         }
+    };
+    using Checked = std::true_type;
+    using Unchecked = std::false_type;
+    float ra[UNROLL][VEC], rb[UNROLL][VEC];
+    bool live[UNROLL];
+    if (PE_PRODUCT_PIPE && HAS_OUTER) {
+        // While every lane of the wave has all UNROLL vectors (a wave's
+        // lanes hold 64 consecutive v), the next iteration's loads are
+        // issued before this iteration's stores: the memory counter
+        // completes in issue order, so waiting for loads issued after a
+        // store would wait for the store as well.
+        const uint32_t vmax = (uint32_t(__builtin_amdgcn_readfirstlane(int(v))) | 63u) + (UNROLL - 1) * stride;
+        const uint32_t step = stride * UNROLL;
+        // (The store flavour is fixed outside the loop: a branch around a
+        // store inside it would make the compiler wait for every load.)
+        // Two register sets in turn (copying one into the other would wait
+        // for the loads just issued), in the order load X0, load Y1, store
+        // X0, load X2, then per pair store Y(i), load Y(i + 2), store
+        // X(i + 1), load X(i + 3): every store's data arrived before the
+        // loads and the store issued after it, which stay in flight, and the
+        // loop is entered in the state it repeats (the compiler takes the
+        // smallest count over the loop's entry and its back edge).
+        auto pipelined = [&](auto nt) {
+            const uint32_t iters = (p.nvec - 1 - vmax) / step + 1;  // wave-uniform
+            const uint32_t v0 = v;
+            float xa[UNROLL][VEC], xb[UNROLL][VEC], ya[UNROLL][VEC], yb[UNROLL][VEC];
+            bool xl[UNROLL], yl[UNROLL];
+            fetch(Unchecked{}, v0, xa, xb, xl);
+            if (iters > 1) {
+                fetch(Unchecked{}, v0 + step, ya, yb, yl);
+                __builtin_amdgcn_sched_barrier(0);
+                finish(Unchecked{}, nt, v0, xa, xb, xl);
+                fetch(Unchecked{}, v0 + 2 * step, xa, xb, xl);
+                uint32_t i = 1;
+                for (; i + 2 <= iters; i += 2) {
+                    finish(Unchecked{}, nt, v0 + i * step, ya, yb, yl);
+                    fetch(Unchecked{}, v0 + (i + 2) * step, ya, yb, yl);
+                    __builtin_amdgcn_sched_barrier(0);
+                    finish(Unchecked{}, nt, v0 + (i + 1) * step, xa, xb, xl);
+                    fetch(Unchecked{}, v0 + (i + 3) * step, xa, xb, xl);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                if (i < iters) finish(Unchecked{}, nt, v0 + i * step, ya, yb, yl);
+            } else {
+                finish(Unchecked{}, nt, v0, xa, xb, xl);
+            }
+            v = v0 + iters * step;
+        };
+        if (vmax < p.nvec) {
+            if (p.nt) pipelined(std::true_type{});
+            else pipelined(std::false_type{});
+        }
+    }
+    for (; v < p.nvec; v += stride * UNROLL) {
+        fetch(Checked{}, v, ra, rb, live);
+        finish(Checked{}, p.nt != 0, v, ra, rb, live);
     }
 }
 
