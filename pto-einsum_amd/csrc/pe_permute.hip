@@ -160,8 +160,13 @@ int tile_edge(bool vstore) {
 #define PE_PERMUTE_NT_MIN_BYTES (32ll << 20)
 #endif
 
+// Tile-transpose blocks per CU in the grid (each walks tiles beyond that):
+// one tile per block up to 64 per CU, so a block's next tile never waits
+// for its last tile's stores (memory counters complete in issue order).
+// Config 2 in0 (12,800 32x32 tiles, one MI355X): 24.5-24.7 us at 32 per CU,
+// 24.2-24.3 at 64, 24.1-24.2 at 128; config 3 in1 unchanged.
 #ifndef PE_TILE_GRID_PER_CU
-#define PE_TILE_GRID_PER_CU 32
+#define PE_TILE_GRID_PER_CU 64
 #endif
 
 // One 64x64 tile per block iteration.  With VLOAD the reads are 16-byte
