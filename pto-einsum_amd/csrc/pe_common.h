@@ -94,6 +94,21 @@ struct F16 {
 #ifndef PE_NT_PARTIAL_MIN_BYTES
 #define PE_NT_PARTIAL_MIN_BYTES (128ll << 20)
 #endif
+// Outputs of at least this many bytes (beyond the 256 MB Infinity Cache)
+// take non-temporal stores at system scope (nt sc0 sc1).  One MI355X,
+// alternating runs on one box: config 3 (2.15 GB) 408-425 -> 394-407 us,
+// its output transpose (2.15 GB) 690-692 -> 661-663 us, 8192^3 float16 NT
+// 904-906 -> 881-890 us (NN unchanged), 4a (268 MB) 133-134 -> 132-133 us;
+// config 5.1's 67 MB output ran slower that way (14.3-15.4 -> 15.8-15.9 us).
+#ifndef PE_NT_SYS_MIN_BYTES
+#define PE_NT_SYS_MIN_BYTES (256ll << 20)
+#endif
+
+// Store flavour of an output of `bytes`: 0 ordinary, 1 non-temporal (from
+// nt_min bytes), 2 non-temporal at system scope.
+inline int nt_mode(int64_t bytes, int64_t nt_min = PE_NT_MIN_BYTES) {
+    return bytes >= PE_NT_SYS_MIN_BYTES ? 2 : bytes >= nt_min ? 1 : 0;
+}
 
 // Non-temporal vector stores (global_store_* ... nt), written as inline
 // assembly: a __builtin_nontemporal_store on one side of a runtime branch
@@ -110,12 +125,22 @@ __device__ __forceinline__ void store_nt(u32x4* p, u32x4 v) {
     asm volatile("global_store_dwordx4 %0, %1, off nt" : : "v"(p), "v"(v) : "memory");
 }
 
-__device__ __forceinline__ void store_f(float* p, float v, bool nt) {
-    if (nt) store_nt(p, v);
-    else *p = v;
+// The same at system scope (store flavour 2).
+__device__ __forceinline__ void store_nt_sys(float* p, float v) {
+    asm volatile("global_store_dword %0, %1, off nt sc0 sc1" : : "v"(p), "v"(v) : "memory");
 }
-__device__ __forceinline__ void store_f(f32x4* p, f32x4 v, bool nt) {
-    if (nt) store_nt(p, v);
+__device__ __forceinline__ void store_nt_sys(f32x4* p, f32x4 v) {
+    asm volatile("global_store_dwordx4 %0, %1, off nt sc0 sc1" : : "v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void store_nt_sys(u32x4* p, u32x4 v) {
+    asm volatile("global_store_dwordx4 %0, %1, off nt sc0 sc1" : : "v"(p), "v"(v) : "memory");
+}
+
+// A store of flavour `mode` (nt_mode).
+template <typename P, typename V>
+__device__ __forceinline__ void store_f(P* p, V v, int mode) {
+    if (mode == 2) store_nt_sys(p, v);
+    else if (mode == 1) store_nt(p, v);
     else *p = v;
 }
 

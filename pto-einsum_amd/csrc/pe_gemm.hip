@@ -139,10 +139,10 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(ReduceArgs r) {
         };
         if constexpr (VST) {
             const f32x4 v = {acc[0], acc[1], acc[2], acc[3]};
-            store_f(reinterpret_cast<f32x4*>(r.c + offset(i * VEC)), v, r.store_nt != 0);
+            store_f(reinterpret_cast<f32x4*>(r.c + offset(i * VEC)), v, r.store_nt);
         } else {
 #pragma unroll
-            for (int e = 0; e < VEC; ++e) store_f(r.c + offset(i * VEC + e), acc[e], r.store_nt != 0);
+            for (int e = 0; e < VEC; ++e) store_f(r.c + offset(i * VEC + e), acc[e], r.store_nt);
         }
     }
 }
@@ -540,7 +540,7 @@ hipError_t launch_res(const pe_gemm_desc& d, const void* a, const void* b, float
     g.nbatch_total = uint32_t(nb);
     g.total_blocks = g.tiles_per_batch * g.nbatch_total;
     g.grid = g.total_blocks;
-    g.store_nt = nb * d.M * d.N * 4 >= PE_NT_MIN_BYTES;
+    g.store_nt = nt_mode(nb * d.M * d.N * 4);
     g.off32 = dl_off32(d);
     g.a_ms = d.a_ms; g.a_ks = d.a_ks; g.b_ks = d.b_ks; g.b_ns = d.b_ns;
     g.c_ms = d.c_ms; g.c_ns = d.c_ns;
@@ -701,7 +701,7 @@ extern "C" int pe_gemm(const pe_gemm_desc* d, const void* a, const void* b, floa
         g.nbatch_total = uint32_t(nb);
         g.total_blocks = g.tiles_per_batch * g.nbatch_total;
         g.grid = g.total_blocks;
-        g.store_nt = nb * d->M * d->N * 4 >= PE_NT_MIN_BYTES;
+        g.store_nt = nt_mode(nb * d->M * d->N * 4);
         g.a_ms = d->a_ms; g.a_ks = d->a_ks; g.b_ks = d->b_ks; g.b_ns = d->b_ns;
         g.c_ms = d->c_ms; g.c_ns = d->c_ns;
         g.nbatch = md.nbatch;
@@ -789,7 +789,7 @@ extern "C" int pe_gemm(const pe_gemm_desc* d, const void* a, const void* b, floa
         g.nbatch_total = uint32_t(nb);
         g.total_blocks = g.tiles_per_batch * g.nbatch_total;
         g.grid = g.total_blocks;
-        g.store_nt = nb * d->M * d->N * 4 >= PE_NT_MIN_BYTES;
+        g.store_nt = nt_mode(nb * d->M * d->N * 4);
         g.a_ms = d->a_ms; g.a_ks = d->a_ks; g.b_ks = d->b_ks; g.b_ns = d->b_ns;
         g.c_ms = d->c_ms; g.c_ns = d->c_ns;
         g.nbatch = d->nbatch;
@@ -814,7 +814,7 @@ extern "C" int pe_gemm(const pe_gemm_desc* d, const void* a, const void* b, floa
     g.nbatch_total = uint32_t(nb);
     g.total_blocks = g.tiles_per_batch * g.nbatch_total * uint32_t(ch.nsplit);
     g.grid = g.total_blocks;
-    g.store_nt = ch.nsplit > 1 ? ch.ws_bytes >= PE_NT_PARTIAL_MIN_BYTES : nb * d->M * d->N * 4 >= PE_NT_MIN_BYTES;
+    g.store_nt = ch.nsplit > 1 ? int(ch.ws_bytes >= PE_NT_PARTIAL_MIN_BYTES) : nt_mode(nb * d->M * d->N * 4);
     g.a_ms = d->a_ms; g.a_ks = d->a_ks; g.b_ks = d->b_ks; g.b_ns = d->b_ns;
     g.c_ms = d->c_ms; g.c_ns = d->c_ns;
     g.nbatch = d->nbatch;
@@ -832,7 +832,7 @@ extern "C" int pe_gemm(const pe_gemm_desc* d, const void* a, const void* b, floa
     if (ch.nsplit > 1) {
         r.nsplit = ch.nsplit;
         r.partial = static_cast<const float*>(ws);
-        r.store_nt = nb * d->M * d->N * 4 >= PE_NT_MIN_BYTES;
+        r.store_nt = nt_mode(nb * d->M * d->N * 4);
         PE_CHECK_HIP(launch_splitk_reduce(r, s));
     }
     return PE_OK;

@@ -52,7 +52,7 @@ constexpr int kBigGroupRows = 4;     // tile rows per walk group
 // dl_store_tile: a wave-uniform 64-bit base in scalar registers, a 32-bit
 // byte offset per lane and one of four uniform row offsets added in the
 // same assembly block.
-template <bool NT, bool MASKED, int FM, int FN>
+template <int NTM, bool MASKED, int FM, int FN>
 __device__ __forceinline__ void big_store_tile(const float* wbase, uint32_t lane_off, uint32_t cms4, uint32_t cns4,
                                                int rrem, int crem, const f32x16 (&acc)[FM][FN]) {
     uint32_t rs[4];
@@ -70,7 +70,11 @@ __device__ __forceinline__ void big_store_tile(const float* wbase, uint32_t lane
                 for (int r = 0; r < 4; ++r) {
                     if (MASKED && 32 * i + 8 * q + r >= rrem) continue;
                     uint32_t t;
-                    if (NT)
+                    if constexpr (NTM == 2)
+                        asm volatile("v_add_u32 %0, %1, %2\n\tglobal_store_dword %0, %3, %4 nt sc0 sc1"
+                                     : "=&v"(t)
+                                     : "s"(rs[r]), "v"(bq), "a"(acc[i][j][4 * q + r]), "s"(wbase));
+                    else if constexpr (NTM == 1)
                         asm volatile("v_add_u32 %0, %1, %2\n\tglobal_store_dword %0, %3, %4 nt"
                                      : "=&v"(t)
                                      : "s"(rs[r]), "v"(bq), "a"(acc[i][j][4 * q + r]), "s"(wbase));
@@ -86,7 +90,7 @@ __device__ __forceinline__ void big_store_tile(const float* wbase, uint32_t lane
 // Output stores of a 128 x 128 wave tile of 16 x 16 accumulator blocks
 // (v_mfma_f32_16x16x32_f16: lane l, register r of block (i, j) holds row
 // 16 i + 4 (l / 16) + r, column 16 j + l % 16), addressed as big_store_tile.
-template <bool NT, bool MASKED>
+template <int NTM, bool MASKED>
 __device__ __forceinline__ void big_store_tile16(const float* wbase, uint32_t lane_off, uint32_t cms4, uint32_t cns4,
                                                  int rrem, int crem, const f32x4 (&acc)[8][8]) {
     uint32_t rs[4];
@@ -102,7 +106,11 @@ __device__ __forceinline__ void big_store_tile16(const float* wbase, uint32_t la
             for (int r = 0; r < 4; ++r) {
                 if (MASKED && 16 * i + r >= rrem) continue;
                 uint32_t t;
-                if (NT)
+                if constexpr (NTM == 2)
+                    asm volatile("v_add_u32 %0, %1, %2\n\tglobal_store_dword %0, %3, %4 nt sc0 sc1"
+                                 : "=&v"(t)
+                                 : "s"(rs[r]), "v"(bq), "a"(acc[i][j][r]), "s"(wbase));
+                else if constexpr (NTM == 1)
                     asm volatile("v_add_u32 %0, %1, %2\n\tglobal_store_dword %0, %3, %4 nt"
                                  : "=&v"(t)
                                  : "s"(rs[r]), "v"(bq), "a"(acc[i][j][r]), "s"(wbase));
@@ -530,7 +538,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_big_kernel(GemmArgs g) {
                 if (__builtin_expect(slab(ya, yb, xa, xb, cs + 1), 0)) break;
             }
 
-            const bool nt = g.store_nt != 0;
+            const int ntm = g.store_nt;  // store flavour (nt_mode)
             float* __restrict__ C = g.c + ct.c_off;
             __builtin_amdgcn_sched_barrier(0);
             asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7");
@@ -543,13 +551,15 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_big_kernel(GemmArgs g) {
             asm volatile("" : "+s"(cms4), "+s"(cns4), "+v"(ln), "+s"(rrem), "+s"(crem));
             const uint32_t lo = (ln >> 4) * 4u * cms4 + (ln & 15u) * cns4;
             if (ct.m0 + BM <= g.M && ct.n0 + BN <= g.N) {
-                if (nt) big_store_tile16<true, false>(wbase, lo, cms4, cns4, 0, 0, acc);
-                else big_store_tile16<false, false>(wbase, lo, cms4, cns4, 0, 0, acc);
+                if (ntm == 2) big_store_tile16<2, false>(wbase, lo, cms4, cns4, 0, 0, acc);
+                else if (ntm == 1) big_store_tile16<1, false>(wbase, lo, cms4, cns4, 0, 0, acc);
+                else big_store_tile16<0, false>(wbase, lo, cms4, cns4, 0, 0, acc);
     
     } else {
             const int rr = rrem - 4 * int(ln >> 4), cr = crem - int(ln & 15u);
-            if (nt) big_store_tile16<true, true>(wbase, lo, cms4, cns4, rr, cr, acc);
-            else big_store_tile16<false, true>(wbase, lo, cms4, cns4, rr, cr, acc);
+            // (partial tiles: the system-scope flavour is not instantiated)
+            if (ntm != 0) big_store_tile16<1, true>(wbase, lo, cms4, cns4, rr, cr, acc);
+            else big_store_tile16<0, true>(wbase, lo, cms4, cns4, rr, cr, acc);
         }
         cbid += walk.step;
         if (cbid >= walk.end) break;
@@ -651,7 +661,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_big_kernel(GemmArgs g) {
             }
 
             // Epilogue: the accumulators straight to the output.
-            const bool nt = g.store_nt != 0;
+            const int ntm = g.store_nt;  // store flavour (nt_mode)
             float* __restrict__ C = g.c + ct.c_off;
             // The store assembly reads accumulators the MFMAs just wrote, a read
             // the compiler cannot see: keep every MFMA above this point and leave
@@ -670,12 +680,14 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_big_kernel(GemmArgs g) {
             asm volatile("" : "+s"(cms4), "+s"(cns4), "+v"(ln), "+s"(rrem), "+s"(crem));
             const uint32_t lo = (ln >> 5) * 4u * cms4 + (ln & 31u) * cns4;
             if (ct.m0 + BM <= g.M && ct.n0 + BN <= g.N) {
-                if (nt) big_store_tile<true, false>(wbase, lo, cms4, cns4, 0, 0, acc);
-                else big_store_tile<false, false>(wbase, lo, cms4, cns4, 0, 0, acc);
+                if (ntm == 2) big_store_tile<2, false>(wbase, lo, cms4, cns4, 0, 0, acc);
+                else if (ntm == 1) big_store_tile<1, false>(wbase, lo, cms4, cns4, 0, 0, acc);
+                else big_store_tile<0, false>(wbase, lo, cms4, cns4, 0, 0, acc);
             } else {
                 const int rr = rrem - 4 * int(ln >> 5), cr = crem - int(ln & 31u);
-                if (nt) big_store_tile<true, true>(wbase, lo, cms4, cns4, rr, cr, acc);
-                else big_store_tile<false, true>(wbase, lo, cms4, cns4, rr, cr, acc);
+                // (partial tiles: the system-scope flavour is not instantiated)
+                if (ntm != 0) big_store_tile<1, true>(wbase, lo, cms4, cns4, rr, cr, acc);
+                else big_store_tile<0, true>(wbase, lo, cms4, cns4, rr, cr, acc);
             }
             cbid += walk.step;
             if (cbid >= walk.end) break;

@@ -65,7 +65,7 @@ namespace pe {
 // and lane values through opaque moves made in the epilogue, so nothing
 // derived from them is hoisted out of the tile loop to hold registers through
 // the MFMA loop.
-template <bool NT, bool MASKED, int FM, int FN>
+template <int NTM, bool MASKED, int FM, int FN>
 __device__ __forceinline__ void dl_store_tile(const float* wbase, uint32_t lane_off, uint32_t cms4, uint32_t cns4,
                                               int rrem, int crem, const f32x16 (&acc)[FM][FN]) {
     uint32_t rs[4];
@@ -83,7 +83,11 @@ __device__ __forceinline__ void dl_store_tile(const float* wbase, uint32_t lane_
                 for (int r = 0; r < 4; ++r) {
                     if (MASKED && 32 * i + 8 * q + r >= rrem) continue;
                     uint32_t t;
-                    if (NT)
+                    if constexpr (NTM == 2)
+                        asm volatile("v_add_u32 %0, %1, %2\n\tglobal_store_dword %0, %3, %4 nt sc0 sc1"
+                                     : "=&v"(t)
+                                     : "s"(rs[r]), "v"(bq), "v"(acc[i][j][4 * q + r]), "s"(wbase));
+                    else if constexpr (NTM == 1)
                         asm volatile("v_add_u32 %0, %1, %2\n\tglobal_store_dword %0, %3, %4 nt"
                                      : "=&v"(t)
                                      : "s"(rs[r]), "v"(bq), "v"(acc[i][j][4 * q + r]), "s"(wbase));
@@ -483,7 +487,7 @@ __global__ __launch_bounds__(kGemmThreads, MINB) void gemm_dl_kernel(GemmArgs g)
     auto epilogue = [&]() {
         float* __restrict__ C;
         int64_t cms, cns;
-        const bool nt = g.store_nt != 0;
+        const int ntm = g.store_nt;  // store flavour (nt_mode)
         if (g.nsplit > 1) {
             C = g.partial + ((int64_t(ct.split) * g.nbatch_total + ct.batch) * g.M) * int64_t(g.N);
             cms = g.N;
@@ -508,12 +512,18 @@ __global__ __launch_bounds__(kGemmThreads, MINB) void gemm_dl_kernel(GemmArgs g)
         asm volatile("" : "+s"(cms4), "+s"(cns4), "+v"(ln), "+s"(rrem), "+s"(crem));
         const uint32_t lo = (ln >> 5) * 4u * cms4 + (ln & 31u) * cns4;
         if (ct.m0 + BM <= g.M && ct.n0 + BN <= g.N) {
-            if (nt) dl_store_tile<true, false>(wbase, lo, cms4, cns4, 0, 0, acc);
-            else dl_store_tile<false, false>(wbase, lo, cms4, cns4, 0, 0, acc);
+            // The system-scope flavour only for float16 operands: a third
+            // epilogue in the float32 kernel shifted its register allocation
+            // (97 -> 96 VGPRs for 128x128 tiles), which let five blocks share
+            // a CU and ran config 2 at 317 against 276 us.
+            if (sizeof(T) == 2 && ntm == 2) dl_store_tile<2, false>(wbase, lo, cms4, cns4, 0, 0, acc);
+            else if (ntm != 0) dl_store_tile<1, false>(wbase, lo, cms4, cns4, 0, 0, acc);
+            else dl_store_tile<0, false>(wbase, lo, cms4, cns4, 0, 0, acc);
         } else {
             const int rr = rrem - 4 * int(ln >> 5), cr = crem - int(ln & 31u);
-            if (nt) dl_store_tile<true, true>(wbase, lo, cms4, cns4, rr, cr, acc);
-            else dl_store_tile<false, true>(wbase, lo, cms4, cns4, rr, cr, acc);
+            // (partial tiles: the system-scope flavour is not instantiated)
+            if (ntm != 0) dl_store_tile<1, true>(wbase, lo, cms4, cns4, rr, cr, acc);
+            else dl_store_tile<0, true>(wbase, lo, cms4, cns4, rr, cr, acc);
         }
 #pragma unroll
         for (int i = 0; i < FM; ++i)
@@ -723,14 +733,16 @@ __global__ __launch_bounds__(kGemmThreads, MINB) void gemm_res_kernel(GemmArgs g
     int rrem = g.M - wm0, crem = g.N - wn0;
     asm volatile("" : "+s"(cms4), "+s"(cns4), "+v"(ln), "+s"(rrem), "+s"(crem));
     const uint32_t lo = (ln >> 5) * 4u * cms4 + (ln & 31u) * cns4;
-    const bool nt = g.store_nt != 0;
+    const int ntm = g.store_nt;  // store flavour (nt_mode)
     if (m0 + BM <= g.M && n0 + BN <= g.N) {
-        if (nt) dl_store_tile<true, false>(wbase, lo, cms4, cns4, 0, 0, acc);
-        else dl_store_tile<false, false>(wbase, lo, cms4, cns4, 0, 0, acc);
+        if (sizeof(T) == 2 && ntm == 2) dl_store_tile<2, false>(wbase, lo, cms4, cns4, 0, 0, acc);
+        else if (ntm != 0) dl_store_tile<1, false>(wbase, lo, cms4, cns4, 0, 0, acc);
+        else dl_store_tile<0, false>(wbase, lo, cms4, cns4, 0, 0, acc);
     } else {
         const int rr = rrem - 4 * int(ln >> 5), cr = crem - int(ln & 31u);
-        if (nt) dl_store_tile<true, true>(wbase, lo, cms4, cns4, rr, cr, acc);
-        else dl_store_tile<false, true>(wbase, lo, cms4, cns4, rr, cr, acc);
+        // (partial tiles: the system-scope flavour is not instantiated)
+        if (ntm != 0) dl_store_tile<1, true>(wbase, lo, cms4, cns4, rr, cr, acc);
+        else dl_store_tile<0, true>(wbase, lo, cms4, cns4, rr, cr, acc);
     }
 }
 

@@ -443,7 +443,7 @@ __global__ __launch_bounds__(kGemmThreads, 2) void gemm_kernel(GemmArgs g) {
         // 8*(r/4) + 4*(l/32) + r%4 and column l%32 of its block.
         float* __restrict__ C;
         int64_t cms, cns;
-        const bool nt = g.store_nt != 0;
+        const int nt = g.store_nt;  // store flavour (nt_mode)
         if (g.nsplit > 1) {
             C = g.partial + ((int64_t(split) * g.nbatch_total + batch) * g.M) * int64_t(g.N);
             cms = g.N;

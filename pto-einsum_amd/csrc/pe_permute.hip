@@ -54,7 +54,7 @@ struct GatherArgs {
     FastDiv outer_div[PE_MAX_DIMS];
     int64_t outer_stride[PE_MAX_DIMS];
     int64_t inner_stride;    // source stride of the innermost destination axis
-    int32_t nt;              // non-temporal stores
+    int32_t nt;              // output store flavour (nt_mode)
 };
 
 template <typename W, int VEC>
@@ -62,10 +62,8 @@ struct Chunk {
     W v[VEC];
 };
 
-__device__ __forceinline__ void put(u32x4* p, const u32x4& v, bool nt) {
-    if (nt) store_nt(p, v);
-    else *p = v;
-}
+// A 16-byte store of flavour `mode` (nt_mode).
+__device__ __forceinline__ void put(u32x4* p, const u32x4& v, int mode) { store_f(p, v, mode); }
 
 // Streamed gather: VEC elements of type W per vector (16 bytes when VEC > 1),
 // U vectors per lane in flight.  Every source vector is read once, with the
@@ -106,7 +104,7 @@ __global__ __launch_bounds__(kThreads) void gather_kernel(GatherArgs p) {
 #pragma unroll
             for (int u = 0; u < U; ++u)
                 if (v0 + u * stride < p.nvec)
-                    put(reinterpret_cast<u32x4*>(dst + int64_t(v0 + u * stride) * VEC), x[u], p.nt != 0);
+                    put(reinterpret_cast<u32x4*>(dst + int64_t(v0 + u * stride) * VEC), x[u], p.nt);
         } else {
 #pragma unroll
             for (int u = 0; u < U; ++u)
@@ -239,7 +237,7 @@ __global__ __launch_bounds__(kThreads) void tile_transpose_kernel(TileArgs p) {
 #pragma unroll
                 for (int j = 0; j < SW; ++j) x.v[j] = tile[sc * SW + j][r];
                 if constexpr (VSTORE)
-                    put(reinterpret_cast<u32x4*>(d), *reinterpret_cast<const u32x4*>(&x), p.nt != 0);
+                    put(reinterpret_cast<u32x4*>(d), *reinterpret_cast<const u32x4*>(&x), p.nt);
             } else {
 #pragma unroll
                 for (int j = 0; j < SW; ++j)
@@ -327,7 +325,7 @@ int run(const pe_permute_desc& d, const void* src, void* dst, hipStream_t s) {
         }
         constexpr int VEC = 16 / sizeof(W);
         constexpr int U = PE_GATHER_UNROLL;
-        a.nt = n * int64_t(sizeof(W)) >= PE_PERMUTE_NT_MIN_BYTES;
+        a.nt = nt_mode(n * int64_t(sizeof(W)), PE_PERMUTE_NT_MIN_BYTES);
         bool vec = inner_kept && nd > 0 && inner % VEC == 0 && aligned(src, 16) && aligned(dst, 16);
         for (int k = 0; k < a.nouter && vec; ++k) vec = sst[k] % VEC == 0;
         const bool outer = a.nouter > 0;
@@ -388,7 +386,7 @@ int run(const pe_permute_desc& d, const void* src, void* dst, hipStream_t s) {
     }
     t.nbatch = nb;
     t.nbatch_total = uint32_t(nbt);
-    t.nt = n * int64_t(sizeof(W)) >= PE_PERMUTE_NT_MIN_BYTES;
+    t.nt = nt_mode(n * int64_t(sizeof(W)), PE_PERMUTE_NT_MIN_BYTES);
     constexpr int VEC = 16 / sizeof(W);
     bool vload = aligned(src, 16) && t.src_q_stride % VEC == 0;
     bool vstore = aligned(dst, 16) && t.dst_p_stride % VEC == 0;

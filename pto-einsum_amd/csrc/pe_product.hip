@@ -71,7 +71,7 @@ struct ProductArgs {
     int64_t a_outer[kMaxOuter];
     int64_t b_outer[kMaxOuter];
     int64_t a_inner, b_inner;
-    int32_t nt;             // non-temporal output stores
+    int32_t nt;             // output store flavour (nt_mode)
     int32_t a_flat;         // A's offset is the output's flat index (A laid out as the output)
     int32_t b_first;        // outer axes below this index have B stride 0 (their index is unused)
 };
@@ -149,7 +149,7 @@ __device__ __forceinline__ void load_b(const typename E::T* b, int64_t off, int6
 }
 
 template <int VEC>
-__device__ __forceinline__ void store_out(float* out, const float (&r)[VEC], bool nt) {
+__device__ __forceinline__ void store_out(float* out, const float (&r)[VEC], int nt) {
     if constexpr (VEC == 4) {
         f32x4 v = {r[0], r[1], r[2], r[3]};
         store_f(reinterpret_cast<f32x4*>(out), v, nt);
@@ -268,7 +268,7 @@ __global__ __launch_bounds__(kThreads) void product_kernel(ProductArgs p) {
                 float prod = xa[u][i] * xb[u][i];
                 r[i] = ADD_ZERO ? 0.0f + prod : prod;
             }
-            if constexpr (std::is_same_v<decltype(nt), bool>)
+            if constexpr (std::is_same_v<decltype(nt), int>)
                 store_out<VEC>(out + int64_t(v0 + u * stride) * VEC, r, nt);
             else
                 store_out_fixed<VEC, decltype(nt)::value>(out + int64_t(v0 + u * stride) * VEC, r);
@@ -328,7 +328,7 @@ __global__ __launch_bounds__(kThreads) void product_kernel(ProductArgs p) {
     }
     for (; v < p.nvec; v += stride * UNROLL) {
         fetch(Checked{}, v, ra, rb, live);
-        finish(Checked{}, p.nt != 0, v, ra, rb, live);
+        finish(Checked{}, p.nt, v, ra, rb, live);
     }
 }
 
@@ -424,7 +424,7 @@ int run(const pe_product_desc& d, const void* in0, const void* in1, float* out,
 
     ProductArgs args{};
     args.a = in0; args.b = in1; args.out = out;
-    args.nt = n * 4 >= PE_NT_MIN_BYTES;
+    args.nt = nt_mode(n * 4);
     const int nd = int(shape.size());
     const int64_t inner = nd ? shape[nd - 1] : 1;
     args.inner = uint32_t(inner);
