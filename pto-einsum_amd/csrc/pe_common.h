@@ -96,10 +96,12 @@ struct F16 {
 #endif
 // Outputs of at least this many bytes (beyond the 256 MB Infinity Cache)
 // take non-temporal stores at system scope (nt sc0 sc1).  One MI355X,
-// alternating runs on one box: config 3 (2.15 GB) 408-425 -> 394-407 us,
-// its output transpose (2.15 GB) 690-692 -> 661-663 us, 8192^3 float16 NT
-// 904-906 -> 881-890 us (NN unchanged), 4a (268 MB) 133-134 -> 132-133 us;
-// config 5.1's 67 MB output ran slower that way (14.3-15.4 -> 15.8-15.9 us).
+// alternating runs on one box (two boxes): config 3 (2.15 GB) 408-425 ->
+// 394-408 us, its output transpose (2.15 GB) 686-692 -> 659-663 us, 8192^3
+// float16 NT 899-906 -> 881-890 us (NN unchanged), 4a (268 MB) 133-134 ->
+// 132-133 us; config 5.1's 67 MB output ran slower that way (14.3-15.4 ->
+// 15.8-15.9 us).  The float32 GEMM epilogues keep the plain non-temporal
+// flavour (pe_gemm_dl.h).
 #ifndef PE_NT_SYS_MIN_BYTES
 #define PE_NT_SYS_MIN_BYTES (256ll << 20)
 #endif
